@@ -1,0 +1,251 @@
+/*
+ * oxihip.h — C-ABI of liboxihip, the MI355X (gfx950) device backend for the
+ * oxitorch layer-kernel hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers, int64 sizes and
+ * scalars, never throws, and returns an `oxi_status`. A non-zero status leaves
+ * a user-facing message in a thread-local slot read by `oxi_hip_last_error()`.
+ * This mirrors the reference error convention (Result inside, exceptions only
+ * at the boundary, no panics across FFI: reference docs/error-handling.md:7-57)
+ * and the variant set of `OxitorchError` (crates/oxi-core/src/lib.rs:186-211).
+ *
+ * All device pointers are HBM buffers obtained from `oxi_hip_alloc`. Float data
+ * is fp32; ids/targets are int64. Launches are asynchronous on one per-process
+ * HIP stream owned by the library; `oxi_hip_sync()` and the d2h copy wait for
+ * it. Output buffers never alias inputs unless an entry point says so.
+ *
+ * Strided entry points take, for each operand, strides in ELEMENTS that are
+ * already broadcast-expanded to the iteration `shape` (stride 0 = broadcast),
+ * i.e. what reference crates/oxi-tensor/src/layout.rs:97-121
+ * (`broadcast_strides`) produces. Rank is at most OXI_MAX_DIMS.
+ */
+#ifndef OXIHIP_H
+#define OXIHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OXI_MAX_DIMS 8
+
+/* Status codes: one per OxitorchError variant (crates/oxi-core/src/lib.rs:186-211).
+ * The caller maps them to Python exceptions as crates/oxi-bindings/src/error.rs:22-32:
+ * 1,2 -> ValueError; 3 -> NotImplementedError; 4,5 -> RuntimeError. */
+typedef enum oxi_status {
+  OXI_OK = 0,
+  OXI_INVALID_ARGUMENT = 1,
+  OXI_SHAPE_MISMATCH = 2,
+  OXI_NOT_IMPLEMENTED = 3,
+  OXI_OUT_OF_BOUNDS = 4,
+  OXI_OTHER = 5
+} oxi_status;
+
+/* Unary registry, same names and order as F32_UNARY_OPS
+ * (crates/oxi-tensor/src/ops.rs:125-202). OXI_UNARY_IDENTITY is a plain copy
+ * (used to materialize views: Tensor::contiguous, lib.rs:230-240). */
+enum {
+  OXI_UNARY_NEG = 0, OXI_UNARY_ABS, OXI_UNARY_SQRT, OXI_UNARY_RSQRT, OXI_UNARY_EXP,
+  OXI_UNARY_LOG, OXI_UNARY_LOG2, OXI_UNARY_LOG10, OXI_UNARY_SIN, OXI_UNARY_COS,
+  OXI_UNARY_TANH, OXI_UNARY_RELU, OXI_UNARY_SIGMOID, OXI_UNARY_FLOOR, OXI_UNARY_CEIL,
+  OXI_UNARY_ROUND, OXI_UNARY_SIGN, OXI_UNARY_SQUARE, OXI_UNARY_RECIPROCAL,
+  OXI_UNARY_IDENTITY, OXI_UNARY_COUNT
+};
+
+/* Binary registry, F32_BINARY_OPS (ops.rs:55-91), then comparisons F32_CMP_OPS
+ * (ops.rs:96-121) which write 1.0f / 0.0f as Tensor::cmp does (lib.rs:284-304). */
+enum {
+  OXI_BINARY_ADD = 0, OXI_BINARY_SUB, OXI_BINARY_MUL, OXI_BINARY_DIV, OXI_BINARY_POW,
+  OXI_BINARY_MIN, OXI_BINARY_MAX,
+  OXI_CMP_EQ, OXI_CMP_NE, OXI_CMP_LT, OXI_CMP_LE, OXI_CMP_GT, OXI_CMP_GE,
+  OXI_BINARY_COUNT
+};
+
+/* Reduction kinds, same order as ReduceKind (ops.rs:222-238). */
+enum {
+  OXI_REDUCE_SUM = 0, OXI_REDUCE_MEAN, OXI_REDUCE_MAX, OXI_REDUCE_MIN,
+  OXI_REDUCE_ARGMAX, OXI_REDUCE_ARGMIN, OXI_REDUCE_NORM
+};
+
+/* VJP mode of the norms. REF reproduces the reference graph, where
+ * `.apply("rsqrt")` detaches the inverse std (python/oxitorch/nn/functional.py:232,239
+ * + crates/oxi-bindings/src/lib.rs:682-710); EXACT is the full derivative. */
+enum { OXI_NORM_VJP_REF = 0, OXI_NORM_VJP_EXACT = 1 };
+
+/* GELU variants: TANH is the reference F.gelu (functional.py:194-199); ERF is
+ * the exact 0.5x(1+erf(x/sqrt2)) that the reference lacks. */
+enum { OXI_GELU_TANH = 0, OXI_GELU_ERF = 1 };
+
+/* ------------------------------------------------------------------------ */
+/* Runtime: device identity, memory, stream.                                */
+/* Replaces the CPU-only device seam: Tensor::device (crates/oxi-tensor/src/lib.rs:192-196),
+ * DeviceBackend/CpuBackend (crates/oxi-tensor/src/ops.rs:294-327) and
+ * device_count (crates/oxi-bindings/src/lib.rs:781-785). */
+
+/* Select and initialise `device`; creates the library stream. Idempotent. */
+int oxi_hip_init(int device);
+/* Number of visible HIP devices (0 when none; not an error). */
+int oxi_hip_device_count(int* count);
+/* Index of the initialised device, or -1. */
+int oxi_hip_current_device(int* device);
+/* Device storage: replaces the Arc<Vec<f32>> buffer (lib.rs:53-58). Blocks are
+ * recycled by a stream-ordered caching allocator. `bytes == 0` yields NULL. */
+int oxi_hip_alloc(size_t bytes, void** out);
+int oxi_hip_free(void* ptr);
+/* Return every cached (free) block to the driver. */
+int oxi_hip_empty_cache(void);
+/* Bytes currently handed out, and bytes held in the cache. */
+int oxi_hip_memory_stats(size_t* in_use, size_t* cached);
+/* Copies. h2d and d2d are stream-ordered; d2h waits for the stream. */
+int oxi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int oxi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int oxi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Wait for all queued work; reports a pending device-side guard (e.g. an id
+ * that escaped host validation) as OXI_OUT_OF_BOUNDS. */
+int oxi_hip_sync(void);
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* oxi_hip_last_error(void);
+/* The library stream (a hipStream_t), for callers that time or order work. */
+int oxi_hip_stream(void** stream);
+/* Events on the library stream, for timing kernels. */
+int oxi_hip_event_create(void** event);
+int oxi_hip_event_record(void* event);
+int oxi_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int oxi_hip_event_destroy(void* event);
+/* Test hook: make the next `n`-th allocation fail (0 disables). */
+int oxi_hip_debug_fail_alloc_after(int n);
+
+/* ------------------------------------------------------------------------ */
+/* Elementwise registry on strided/broadcast operands.                      */
+
+/* y = fill value (n contiguous floats). Used for Tensor::zeros/full
+ * (lib.rs:67-158) and the scalar-operand promotion of const_full
+ * (crates/oxi-bindings/src/lib.rs:86-89). Kernel fill, safe under graph capture. */
+int oxi_fill(float* y, int64_t n, float value);
+
+/* y[i] = op(x[i]) over `shape`. Replaces Tensor::unary / unary_op
+ * (crates/oxi-tensor/src/lib.rs:306-325,353-357) and iterate::map_n
+ * (crates/oxi-tensor/src/iterate.rs:21-75). */
+int oxi_unary(int op, const float* x, const int64_t* x_strides,
+              float* y, const int64_t* y_strides,
+              const int64_t* shape, int ndim);
+
+/* y[i] = a[i] op b[i] with broadcast strides. Replaces Tensor::binary /
+ * binary_op / cmp_op (crates/oxi-tensor/src/lib.rs:263-304,332-347). */
+int oxi_binary(int op, const float* a, const int64_t* a_strides,
+               const float* b, const int64_t* b_strides,
+               float* y, const int64_t* y_strides,
+               const int64_t* shape, int ndim);
+
+/* ------------------------------------------------------------------------ */
+/* Fused activations (strided, one graph node each).                         */
+
+/* F.gelu (python/oxitorch/nn/functional.py:194-199), `approximate` = OXI_GELU_*. */
+int oxi_gelu_fwd(const float* x, const int64_t* x_strides,
+                 float* y, const int64_t* y_strides,
+                 const int64_t* shape, int ndim, int approximate);
+/* dx = g * gelu'(x). For OXI_GELU_TANH the arithmetic follows the composed VJP
+ * of the reference graph (mul/add/tanh VJPs, crates/oxi-autograd/src/ops.rs:62-73,218-230). */
+int oxi_gelu_bwd(const float* x, const int64_t* x_strides,
+                 const float* g, const int64_t* g_strides,
+                 float* dx, const int64_t* dx_strides,
+                 const int64_t* shape, int ndim, int approximate);
+/* F.silu = x * sigmoid(x) (functional.py:202-204). */
+int oxi_silu_fwd(const float* x, const int64_t* x_strides,
+                 float* y, const int64_t* y_strides,
+                 const int64_t* shape, int ndim);
+/* dx = g*s + (g*x)*(s*(1-s)), the mul VJP (ops.rs:62-73) plus the sigmoid VJP (ops.rs:236-247). */
+int oxi_silu_bwd(const float* x, const int64_t* x_strides,
+                 const float* g, const int64_t* g_strides,
+                 float* dx, const int64_t* dx_strides,
+                 const int64_t* shape, int ndim);
+
+/* ------------------------------------------------------------------------ */
+/* Norms over the last dim of a contiguous (rows, cols) buffer.              */
+
+/* F.rms_norm (functional.py:236-240): y = (x*inv)*w, inv = 1/sqrt(mean(x*x)+eps).
+ * Writes the per-row `rstd` (= inv) for the backward. */
+int oxi_rms_norm_fwd(const float* x, const float* w, float* y, float* rstd,
+                     int64_t rows, int64_t cols, float eps);
+/* RMS VJP. mode REF: dx = (g*w)*inv; EXACT: dx = inv*(g*w - xhat*mean(g*w*xhat)).
+ * dw = sum over rows of g*(x*inv) (unbroadcast, crates/oxi-autograd/src/graph.rs:274-313).
+ * dx or dw may be NULL to skip. Deterministic (no float atomics). */
+int oxi_rms_norm_bwd(const float* x, const float* w, const float* rstd, const float* g,
+                     float* dx, float* dw, int64_t rows, int64_t cols, int mode);
+/* F.layer_norm (functional.py:227-233): y = ((x-mu)*inv)*w + b. w/b may be NULL
+ * (no affine). Writes per-row mean and rstd. */
+int oxi_layer_norm_fwd(const float* x, const float* w, const float* b, float* y,
+                       float* mean, float* rstd, int64_t rows, int64_t cols, float eps);
+/* LN VJP. mode REF: dx = gc - mean_row(gc), gc = (g*w)*inv; EXACT: the full
+ * derivative. dw = sum_rows g*((x-mu)*inv), db = sum_rows g. dx/dw/db may be NULL. */
+int oxi_layer_norm_bwd(const float* x, const float* w, const float* mean, const float* rstd,
+                       const float* g, float* dx, float* dw, float* db,
+                       int64_t rows, int64_t cols, int mode);
+
+/* ------------------------------------------------------------------------ */
+/* Softmax family over the middle dim of a contiguous (outer, len, inner)    */
+/* buffer (inner == 1 is the last-dim case).                                 */
+
+/* F.softmax (functional.py:211-215). */
+int oxi_softmax_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inner);
+/* dx = y*(g - sum(g*y)). */
+int oxi_softmax_bwd(const float* y, const float* g, float* dx,
+                    int64_t outer, int64_t len, int64_t inner);
+/* F.log_softmax (functional.py:218-222). */
+int oxi_log_softmax_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inner);
+/* dx = g - exp(y)*sum(g). */
+int oxi_log_softmax_bwd(const float* y, const float* g, float* dx,
+                        int64_t outer, int64_t len, int64_t inner);
+/* F.cross_entropy, mean reduction (functional.py:277-293), fused: writes the
+ * scalar loss (1 float on device) and the per-row log-sum-exp `lse` (n floats).
+ * `targets` are int64 class ids already resolved to [0, c). */
+int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets,
+                          float* loss, float* lse, int64_t n, int64_t c);
+/* dlogits = (softmax(logits) - onehot(targets)) * gloss[0] / n. `gloss` is a
+ * device pointer to the upstream scalar gradient. */
+int oxi_cross_entropy_bwd(const float* logits, const int64_t* targets, const float* lse,
+                          const float* gloss, float* dlogits, int64_t n, int64_t c);
+
+/* ------------------------------------------------------------------------ */
+/* Gather / scatter-add.                                                     */
+
+/* out[o, k, i] = src[o, idx[k], i] for a contiguous (outer, len, inner) source.
+ * `idx` (n int64 on device) may hold negatives in [-len, len), which wrap.
+ * Replaces Tensor::index_select (crates/oxi-tensor/src/lib.rs:665-703); ids are
+ * also validated on the host, this kernel only guards (see oxi_hip_sync). */
+int oxi_index_select(const float* src, int64_t outer, int64_t len, int64_t inner,
+                     const int64_t* idx, int64_t n, float* out);
+/* Dense VJP of index_select: grad_src[o, v, i] = sum over k with idx[k]==v of
+ * g[o, k, i], accumulated in position order k per id (a stable counting sort
+ * by id plus a segmented reduction; no atomics on floats). Every element of
+ * `grad_src` (outer*len*inner) is written. Replaces scatter_index_select
+ * (crates/oxi-autograd/src/ops.rs:741-769). */
+int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inner,
+                         const int64_t* idx, int64_t n, float* grad_src);
+/* F.embedding (functional.py:245-247) = index_select on dim 0 of W (V, D). */
+int oxi_embedding_fwd(const float* W, const int64_t* ids, int64_t n,
+                      int64_t V, int64_t D, float* out);
+/* dW (V, D) = dense duplicate-accumulating VJP of F.embedding. */
+int oxi_embedding_bwd(const float* g, const int64_t* ids, int64_t n,
+                      int64_t V, int64_t D, float* dW);
+
+/* ------------------------------------------------------------------------ */
+/* Dim reductions.                                                           */
+
+/* Reduce a strided tensor along `dim` into a contiguous output of
+ * prod(shape)/shape[dim] floats (row-major over the remaining dims).
+ * Semantics of ReduceKind::reduce_strip (crates/oxi-tensor/src/ops.rs:246-285):
+ * MAX/MIN ignore NaN (fold with f32::max/min), ARGMAX/ARGMIN keep the first
+ * strict winner starting from index 0, indices are written as floats
+ * (Tensor::reduce, crates/oxi-tensor/src/lib.rs:519-576). Empty dims: SUM/MEAN/NORM
+ * give 0, the others return OXI_INVALID_ARGUMENT. Replaces Tensor::reduce. */
+int oxi_reduce(int kind, const float* x, const int64_t* x_strides,
+               const int64_t* shape, int ndim, int dim, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OXIHIP_H */

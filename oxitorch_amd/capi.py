@@ -1,0 +1,393 @@
+"""ctypes binding of liboxihip's C-ABI (include/oxihip.h).
+
+This is the thin Python-side FFI a host binds to reach the MI355X kernels:
+`DeviceArray` owns an HBM buffer from the library's caching allocator, and
+each launcher takes DeviceArrays and plain sizes. Status codes are mapped to
+exceptions exactly as the reference maps OxitorchError variants
+(crates/oxi-bindings/src/error.rs:22-32): invalid argument / shape mismatch ->
+ValueError, not implemented -> NotImplementedError, out of bounds / other ->
+RuntimeError, each carrying the library's message.
+
+There is no CPU fallback: if liboxihip.so is missing, importing this module
+raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("OXIHIP_LIB", _HERE / "liboxihip.so"))
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"liboxihip.so not found at {LIB_PATH}: build it with `python -m oxitorch_amd.build lib` "
+        "(the device path has no CPU fallback)"
+    )
+
+lib = ctypes.CDLL(str(LIB_PATH))
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_float = ctypes.c_float
+c_size = ctypes.c_size_t
+vp = ctypes.c_void_p
+P_i64 = ctypes.POINTER(ctypes.c_int64)
+
+# status codes (oxi_status)
+OK, INVALID_ARGUMENT, SHAPE_MISMATCH, NOT_IMPLEMENTED, OUT_OF_BOUNDS, OTHER = range(6)
+
+UNARY = ["neg", "abs", "sqrt", "rsqrt", "exp", "log", "log2", "log10", "sin", "cos", "tanh", "relu", "sigmoid",
+         "floor", "ceil", "round", "sign", "square", "reciprocal", "identity"]
+BINARY = ["add", "sub", "mul", "div", "pow", "min", "max", "eq", "ne", "lt", "le", "gt", "ge"]
+REDUCE = ["sum", "mean", "max", "min", "argmax", "argmin", "norm"]
+NORM_VJP = {"ref": 0, "exact": 1}
+GELU = {"tanh": 0, "none": 1, "erf": 1}
+
+_SIGS = {
+    "oxi_hip_init": [c_int],
+    "oxi_hip_device_count": [ctypes.POINTER(c_int)],
+    "oxi_hip_current_device": [ctypes.POINTER(c_int)],
+    "oxi_hip_alloc": [c_size, ctypes.POINTER(vp)],
+    "oxi_hip_free": [vp],
+    "oxi_hip_empty_cache": [],
+    "oxi_hip_memory_stats": [ctypes.POINTER(c_size), ctypes.POINTER(c_size)],
+    "oxi_hip_memcpy_h2d": [vp, vp, c_size],
+    "oxi_hip_memcpy_d2h": [vp, vp, c_size],
+    "oxi_hip_memcpy_d2d": [vp, vp, c_size],
+    "oxi_hip_sync": [],
+    "oxi_hip_stream": [ctypes.POINTER(vp)],
+    "oxi_hip_event_create": [ctypes.POINTER(vp)],
+    "oxi_hip_event_record": [vp],
+    "oxi_hip_event_elapsed_ms": [vp, vp, ctypes.POINTER(c_float)],
+    "oxi_hip_event_destroy": [vp],
+    "oxi_hip_debug_fail_alloc_after": [c_int],
+    "oxi_fill": [vp, c_i64, c_float],
+    "oxi_unary": [c_int, vp, P_i64, vp, P_i64, P_i64, c_int],
+    "oxi_binary": [c_int, vp, P_i64, vp, P_i64, vp, P_i64, P_i64, c_int],
+    "oxi_gelu_fwd": [vp, P_i64, vp, P_i64, P_i64, c_int, c_int],
+    "oxi_gelu_bwd": [vp, P_i64, vp, P_i64, vp, P_i64, P_i64, c_int, c_int],
+    "oxi_silu_fwd": [vp, P_i64, vp, P_i64, P_i64, c_int],
+    "oxi_silu_bwd": [vp, P_i64, vp, P_i64, vp, P_i64, P_i64, c_int],
+    "oxi_rms_norm_fwd": [vp, vp, vp, vp, c_i64, c_i64, c_float],
+    "oxi_rms_norm_bwd": [vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
+    "oxi_layer_norm_fwd": [vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_float],
+    "oxi_layer_norm_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
+    "oxi_softmax_fwd": [vp, vp, c_i64, c_i64, c_i64],
+    "oxi_softmax_bwd": [vp, vp, vp, c_i64, c_i64, c_i64],
+    "oxi_log_softmax_fwd": [vp, vp, c_i64, c_i64, c_i64],
+    "oxi_log_softmax_bwd": [vp, vp, vp, c_i64, c_i64, c_i64],
+    "oxi_cross_entropy_fwd": [vp, vp, vp, vp, c_i64, c_i64],
+    "oxi_cross_entropy_bwd": [vp, vp, vp, vp, vp, c_i64, c_i64],
+    "oxi_index_select": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
+    "oxi_index_select_bwd": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
+    "oxi_embedding_fwd": [vp, vp, c_i64, c_i64, c_i64, vp],
+    "oxi_embedding_bwd": [vp, vp, c_i64, c_i64, c_i64, vp],
+    "oxi_reduce": [c_int, vp, P_i64, P_i64, c_int, c_int, vp],
+}
+
+for _name, _args in _SIGS.items():
+    _fn = getattr(lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = c_int
+lib.oxi_hip_last_error.argtypes = []
+lib.oxi_hip_last_error.restype = ctypes.c_char_p
+
+DECLARED = sorted(list(_SIGS) + ["oxi_hip_last_error"])
+
+
+class OxiError(RuntimeError):
+    pass
+
+
+def last_error() -> str:
+    return lib.oxi_hip_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = last_error()
+    if rc in (INVALID_ARGUMENT, SHAPE_MISMATCH):
+        raise ValueError(msg)
+    if rc == NOT_IMPLEMENTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib, name)(*args))
+
+
+def device_count() -> int:
+    n = c_int(0)
+    check(lib.oxi_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def init(device: int = 0) -> None:
+    check(lib.oxi_hip_init(device))
+
+
+def sync() -> None:
+    check(lib.oxi_hip_sync())
+
+
+def memory_stats() -> tuple[int, int]:
+    a, b = c_size(0), c_size(0)
+    check(lib.oxi_hip_memory_stats(ctypes.byref(a), ctypes.byref(b)))
+    return a.value, b.value
+
+
+def _i64arr(vals) -> ctypes.Array:
+    vals = [int(v) for v in vals]
+    return (ctypes.c_int64 * max(1, len(vals)))(*vals)
+
+
+class DeviceArray:
+    """An HBM buffer of fp32 or int64 elements with a shape (row-major)."""
+
+    __slots__ = ("ptr", "shape", "dtype", "nbytes", "__weakref__")
+
+    def __init__(self, shape, dtype=np.float32):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = vp()
+        check(lib.oxi_hip_alloc(self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        if d.nbytes:
+            check(lib.oxi_hip_memcpy_h2d(d.ptr, a.ctypes.data, d.nbytes))
+        return d
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            check(lib.oxi_hip_memcpy_d2h(out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    @property
+    def size(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64))
+
+    def free(self) -> None:
+        if self.ptr:
+            lib.oxi_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def row_major_strides(shape):
+    st = [1] * len(shape)
+    for d in range(len(shape) - 2, -1, -1):
+        st[d] = st[d + 1] * shape[d + 1]
+    return st
+
+
+# ---- launchers (DeviceArray in, DeviceArray out) -----------------------------
+
+def unary(name: str, x: DeviceArray, out: DeviceArray | None = None, x_strides=None, shape=None) -> DeviceArray:
+    shape = tuple(shape or x.shape)
+    out = out or DeviceArray(shape)
+    xs = x_strides or row_major_strides(shape)
+    call("oxi_unary", UNARY.index(name), x.ptr, _i64arr(xs), out.ptr, _i64arr(row_major_strides(shape)),
+         _i64arr(shape), len(shape))
+    return out
+
+
+def binary(name: str, a: DeviceArray, b: DeviceArray, a_strides, b_strides, shape,
+           out: DeviceArray | None = None) -> DeviceArray:
+    shape = tuple(shape)
+    out = out or DeviceArray(shape)
+    call("oxi_binary", BINARY.index(name), a.ptr, _i64arr(a_strides), b.ptr, _i64arr(b_strides), out.ptr,
+         _i64arr(row_major_strides(shape)), _i64arr(shape), len(shape))
+    return out
+
+
+def gelu_fwd(x: DeviceArray, approximate="tanh", out=None, x_strides=None, shape=None) -> DeviceArray:
+    shape = tuple(shape or x.shape)
+    out = out or DeviceArray(shape)
+    call("oxi_gelu_fwd", x.ptr, _i64arr(x_strides or row_major_strides(shape)), out.ptr,
+         _i64arr(row_major_strides(shape)), _i64arr(shape), len(shape), GELU[approximate])
+    return out
+
+
+def gelu_bwd(x: DeviceArray, g: DeviceArray, approximate="tanh", out=None, x_strides=None, g_strides=None,
+             shape=None) -> DeviceArray:
+    shape = tuple(shape or x.shape)
+    out = out or DeviceArray(shape)
+    rm = row_major_strides(shape)
+    call("oxi_gelu_bwd", x.ptr, _i64arr(x_strides or rm), g.ptr, _i64arr(g_strides or rm), out.ptr, _i64arr(rm),
+         _i64arr(shape), len(shape), GELU[approximate])
+    return out
+
+
+def silu_fwd(x: DeviceArray, out=None, x_strides=None, shape=None) -> DeviceArray:
+    shape = tuple(shape or x.shape)
+    out = out or DeviceArray(shape)
+    rm = row_major_strides(shape)
+    call("oxi_silu_fwd", x.ptr, _i64arr(x_strides or rm), out.ptr, _i64arr(rm), _i64arr(shape), len(shape))
+    return out
+
+
+def silu_bwd(x: DeviceArray, g: DeviceArray, out=None, x_strides=None, g_strides=None, shape=None) -> DeviceArray:
+    shape = tuple(shape or x.shape)
+    out = out or DeviceArray(shape)
+    rm = row_major_strides(shape)
+    call("oxi_silu_bwd", x.ptr, _i64arr(x_strides or rm), g.ptr, _i64arr(g_strides or rm), out.ptr, _i64arr(rm),
+         _i64arr(shape), len(shape))
+    return out
+
+
+def _rows(x: DeviceArray):
+    H = x.shape[-1] if x.shape else 1
+    return (x.size // H if H else 0), H
+
+
+def rms_norm_fwd(x: DeviceArray, w: DeviceArray, eps=1e-6):
+    rows, H = _rows(x)
+    y = DeviceArray(x.shape)
+    rstd = DeviceArray((rows,))
+    call("oxi_rms_norm_fwd", x.ptr, w.ptr, y.ptr, rstd.ptr, rows, H, eps)
+    return y, rstd
+
+
+def rms_norm_bwd(x, w, rstd, g, mode="ref", need_dx=True, need_dw=True):
+    rows, H = _rows(x)
+    dx = DeviceArray(x.shape) if need_dx else None
+    dw = DeviceArray((H,)) if need_dw else None
+    call("oxi_rms_norm_bwd", x.ptr, w.ptr, rstd.ptr, g.ptr, dx.ptr if dx else None, dw.ptr if dw else None, rows, H,
+         NORM_VJP[mode])
+    return dx, dw
+
+
+def layer_norm_fwd(x: DeviceArray, w: DeviceArray | None, b: DeviceArray | None, eps=1e-5):
+    rows, H = _rows(x)
+    y = DeviceArray(x.shape)
+    mean = DeviceArray((rows,))
+    rstd = DeviceArray((rows,))
+    call("oxi_layer_norm_fwd", x.ptr, w.ptr if w else None, b.ptr if b else None, y.ptr, mean.ptr, rstd.ptr, rows,
+         H, eps)
+    return y, mean, rstd
+
+
+def layer_norm_bwd(x, w, mean, rstd, g, mode="ref", need_dx=True, need_dw=True, need_db=True):
+    rows, H = _rows(x)
+    dx = DeviceArray(x.shape) if need_dx else None
+    dw = DeviceArray((H,)) if need_dw else None
+    db = DeviceArray((H,)) if need_db else None
+    call("oxi_layer_norm_bwd", x.ptr, w.ptr if w else None, mean.ptr, rstd.ptr, g.ptr, dx.ptr if dx else None,
+         dw.ptr if dw else None, db.ptr if db else None, rows, H, NORM_VJP[mode])
+    return dx, dw, db
+
+
+def _oli(shape, dim):
+    dim = dim % len(shape)
+    outer = int(np.prod(shape[:dim], dtype=np.int64))
+    inner = int(np.prod(shape[dim + 1:], dtype=np.int64))
+    return outer, shape[dim], inner
+
+
+def softmax_fwd(x: DeviceArray, dim=-1, log=False) -> DeviceArray:
+    y = DeviceArray(x.shape)
+    call("oxi_log_softmax_fwd" if log else "oxi_softmax_fwd", x.ptr, y.ptr, *_oli(x.shape, dim))
+    return y
+
+
+def softmax_bwd(y: DeviceArray, g: DeviceArray, dim=-1, log=False) -> DeviceArray:
+    dx = DeviceArray(y.shape)
+    call("oxi_log_softmax_bwd" if log else "oxi_softmax_bwd", y.ptr, g.ptr, dx.ptr, *_oli(y.shape, dim))
+    return dx
+
+
+def cross_entropy_fwd(logits: DeviceArray, targets: DeviceArray):
+    n, c = logits.shape
+    loss = DeviceArray((1,))
+    lse = DeviceArray((n,))
+    call("oxi_cross_entropy_fwd", logits.ptr, targets.ptr, loss.ptr, lse.ptr, n, c)
+    return loss, lse
+
+
+def cross_entropy_bwd(logits: DeviceArray, targets: DeviceArray, lse: DeviceArray, gloss: DeviceArray):
+    n, c = logits.shape
+    d = DeviceArray((n, c))
+    call("oxi_cross_entropy_bwd", logits.ptr, targets.ptr, lse.ptr, gloss.ptr, d.ptr, n, c)
+    return d
+
+
+def index_select(src: DeviceArray, dim: int, idx: DeviceArray) -> DeviceArray:
+    o, l, i = _oli(src.shape, dim)
+    shape = list(src.shape)
+    shape[dim % len(shape)] = idx.size
+    out = DeviceArray(shape)
+    call("oxi_index_select", src.ptr, o, l, i, idx.ptr, idx.size, out.ptr)
+    return out
+
+
+def index_select_bwd(g: DeviceArray, full_shape, dim: int, idx: DeviceArray) -> DeviceArray:
+    o, l, i = _oli(tuple(full_shape), dim)
+    grad = DeviceArray(full_shape)
+    call("oxi_index_select_bwd", g.ptr, o, l, i, idx.ptr, idx.size, grad.ptr)
+    return grad
+
+
+def embedding_fwd(W: DeviceArray, ids: DeviceArray) -> DeviceArray:
+    V, D = W.shape
+    out = DeviceArray((ids.size, D))
+    call("oxi_embedding_fwd", W.ptr, ids.ptr, ids.size, V, D, out.ptr)
+    return out
+
+
+def embedding_bwd(g: DeviceArray, ids: DeviceArray, V: int) -> DeviceArray:
+    D = g.shape[-1]
+    dW = DeviceArray((V, D))
+    call("oxi_embedding_bwd", g.ptr, ids.ptr, ids.size, V, D, dW.ptr)
+    return dW
+
+
+def reduce(kind: str, x: DeviceArray, dim: int, x_strides=None, shape=None) -> DeviceArray:
+    shape = tuple(shape or x.shape)
+    dim = dim % len(shape)
+    out = DeviceArray(shape[:dim] + shape[dim + 1:])
+    call("oxi_reduce", REDUCE.index(kind), x.ptr, _i64arr(x_strides or row_major_strides(shape)), _i64arr(shape),
+         len(shape), dim, out.ptr)
+    return out
+
+
+class Timer:
+    """HIP events on the library stream (the stream every kernel runs on)."""
+
+    def __init__(self):
+        self.a, self.b = vp(), vp()
+        check(lib.oxi_hip_event_create(ctypes.byref(self.a)))
+        check(lib.oxi_hip_event_create(ctypes.byref(self.b)))
+
+    def start(self):
+        check(lib.oxi_hip_event_record(self.a))
+
+    def stop(self) -> float:
+        check(lib.oxi_hip_event_record(self.b))
+        ms = c_float(0.0)
+        check(lib.oxi_hip_event_elapsed_ms(self.a, self.b, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            lib.oxi_hip_event_destroy(self.a)
+            lib.oxi_hip_event_destroy(self.b)
+        except Exception:
+            pass

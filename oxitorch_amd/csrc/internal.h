@@ -1,0 +1,108 @@
+// Internal helpers shared by the liboxihip translation units: status/error
+// plumbing, the library stream, workspace allocation and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+#include "oxihip.h"
+
+namespace oxi {
+
+// Sets the thread-local error message and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps a failing HIP call to OXI_OTHER with its name and HIP error string.
+int fail_hip(hipError_t err, const char* what);
+// Stream of the initialised device; initialises device 0 on first use.
+// Returns nullptr and sets the error when no device can be initialised.
+bool ensure_init();
+hipStream_t stream();
+// Workspace from the caching allocator (stream-ordered reuse, no sync).
+void* ws_alloc(size_t bytes);
+void ws_free(void* p);
+// Device-side guard flag: kernels that meet an index outside its range set it;
+// oxi_hip_sync() reports it. Pointer to one int in device memory.
+int* guard_flag();
+// Checks the launch that just happened.
+int check_launch(const char* what);
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Number of compute units of the current device (cached).
+int cu_count();
+
+// A small RAII workspace holder.
+struct Workspace {
+  void* p = nullptr;
+  explicit Workspace(size_t bytes) : p(bytes ? ws_alloc(bytes) : nullptr) {}
+  ~Workspace() { if (p) ws_free(p); }
+  Workspace(const Workspace&) = delete;
+  Workspace& operator=(const Workspace&) = delete;
+  template <typename T> T* as() const { return static_cast<T*>(p); }
+};
+
+}  // namespace oxi
+
+#define OXI_CHECK_INIT()                                   \
+  do {                                                     \
+    if (!oxi::ensure_init()) return OXI_OTHER;             \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Device-side reductions over a wave64 (CDNA: 64 lanes per wavefront).
+
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
+namespace oxi {
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+// Sum across the `TPR` threads of a row group. TPR is 64 (one wave, no LDS)
+// or a multiple of 64 equal to the block size (LDS combine in fixed order, so
+// every thread gets the same, deterministic result). `lds` holds TPR/64 floats.
+template <int TPR, typename T>
+__device__ __forceinline__ T group_sum(T v, T* lds) {
+  v = wave_sum(v);
+  if constexpr (TPR > 64) {
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    v = lds[0];
+#pragma unroll
+    for (int i = 1; i < TPR / 64; ++i) v += lds[i];
+  }
+  return v;
+}
+
+template <int TPR>
+__device__ __forceinline__ float group_max(float v, float* lds) {
+  v = wave_max(v);
+  if constexpr (TPR > 64) {
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    v = lds[0];
+#pragma unroll
+    for (int i = 1; i < TPR / 64; ++i) v = fmaxf(v, lds[i]);
+  }
+  return v;
+}
+
+}  // namespace oxi
+#endif

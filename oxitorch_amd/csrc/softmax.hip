@@ -1,0 +1,489 @@
+// Softmax, log-softmax and fused cross-entropy kernels for gfx950.
+//
+// Softmax-family ops reduce over the middle dim of a contiguous
+// (outer, len, inner) buffer. inner == 1 (the last dim, the hot case) runs one
+// row per row group with the row held in registers when it fits
+// (len <= 8192, 16-byte aligned), so x is read once and y written once;
+// longer rows stream twice (online max/sum pass, then the write pass).
+// inner > 1 runs one thread per (outer, inner) column, coalesced across inner.
+//
+// Cross-entropy (mean reduction) is fused into two kernels: the forward streams
+// each logits row once with an online (max, sum-exp) and writes the row's
+// log-sum-exp plus its picked log-probability; a one-block kernel forms the
+// mean in float64 in fixed order. The backward streams logits once more and
+// writes (softmax - onehot) * g / n. Bytes per row: 1 read fwd, 1 read + 1
+// write bwd, instead of the reference's dense one-hot and ~16 passes
+// (python/oxitorch/nn/functional.py:277-293).
+#include <cmath>
+
+#include "internal.h"
+#include "rowtile.h"
+
+namespace oxi {
+namespace {
+
+constexpr int BS = 256;
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+__device__ __forceinline__ float max4(const f4& v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
+__device__ __forceinline__ float sum4(const f4& v) { return (v.x + v.y) + (v.z + v.w); }
+__device__ __forceinline__ f4 exp4(const f4& v) { return f4{expf(v.x), expf(v.y), expf(v.z), expf(v.w)}; }
+
+// Running (max, sum of exp(v - max)) of one thread; `m == -inf` means no
+// finite contribution yet (sum 0).
+struct Online {
+  float m = NEG_INF;
+  float s = 0.f;
+  __device__ __forceinline__ void add4(const f4& v) {
+    const float cm = max4(v);
+    if (cm > m) {
+      s = (m == NEG_INF) ? 0.f : s * expf(m - cm);
+      m = cm;
+    }
+    if (m != NEG_INF) s += sum4(exp4(v - m));
+    else if (cm != cm || v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) s = __builtin_nanf("");
+  }
+  __device__ __forceinline__ void add1(float v) {
+    if (v > m) {
+      s = (m == NEG_INF) ? 0.f : s * expf(m - v);
+      m = v;
+    }
+    if (m != NEG_INF) s += expf(v - m);
+    else if (v != v) s = __builtin_nanf("");
+  }
+};
+
+// Combine the Online states of a row group; every thread gets (M, S).
+template <int TPR>
+__device__ __forceinline__ void group_online(Online& o, float* lds) {
+  const float M = group_max<TPR>(o.m, lds);
+  float part = (o.m == NEG_INF) ? ((o.s != o.s) ? o.s : 0.f) : o.s * expf(o.m - M);
+  const float S = group_sum<TPR, float>(part, lds + BS / 64);
+  o.m = M;
+  o.s = S;
+}
+
+// ---------------------------------------------------------------------------
+// Last-dim kernels, register-resident rows.
+
+template <int TPR, int NV, bool LOG>
+__global__ __launch_bounds__(BS) void sm_fwd_k(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int H) {
+  constexpr int GPB = BS / TPR;
+  __shared__ float lds[2 * (BS / 64)];
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * GPB + threadIdx.x / TPR;
+  if (row >= rows) return;
+  const int h4 = H >> 2;
+  RowTile<TPR, NV> xt;
+  xt.load(x + row * H, h4, t);
+  float m = NEG_INF;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if (k * TPR + t < h4) m = fmaxf(m, max4(xt.v[k]));
+  m = group_max<TPR>(m, lds);
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    if (k * TPR + t < h4) {
+      const f4 z = xt.v[k] - m;
+      const f4 e = exp4(z);
+      s += sum4(e);
+      xt.v[k] = LOG ? z : e;
+    }
+  }
+  s = group_sum<TPR, float>(s, lds + BS / 64);
+  if constexpr (LOG) {
+    const float L = logf(s);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) xt.v[k] = xt.v[k] - L;
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) xt.v[k] = xt.v[k] / s;
+  }
+  xt.store(y + row * H, h4, t);
+}
+
+template <int TPR, int NV, bool LOG>
+__global__ __launch_bounds__(BS) void sm_bwd_k(const float* __restrict__ y, const float* __restrict__ g,
+                                               float* __restrict__ dx, int64_t rows, int H) {
+  constexpr int GPB = BS / TPR;
+  __shared__ float lds[BS / 64];
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * GPB + threadIdx.x / TPR;
+  if (row >= rows) return;
+  const int h4 = H >> 2;
+  RowTile<TPR, NV> yt, gt;
+  yt.load(y + row * H, h4, t);
+  gt.load(g + row * H, h4, t);
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) s += LOG ? sum4(gt.v[k]) : sum4(gt.v[k] * yt.v[k]);
+  s = group_sum<TPR, float>(s, lds);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    if constexpr (LOG) gt.v[k] = gt.v[k] - exp4(yt.v[k]) * s;
+    else gt.v[k] = yt.v[k] * (gt.v[k] - s);
+  }
+  gt.store(dx + row * H, h4, t);
+}
+
+// Last-dim kernels for any length / alignment: one block per row, two passes.
+template <bool LOG>
+__global__ __launch_bounds__(BS) void sm_fwd_loop_k(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int H) {
+  __shared__ float lds[2 * (BS / 64)];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * H;
+  Online o;
+  for (int c = threadIdx.x; c < H; c += BS) o.add1(xr[c]);
+  group_online<BS>(o, lds);
+  float* yr = y + row * H;
+  const float L = logf(o.s);
+  for (int c = threadIdx.x; c < H; c += BS) {
+    const float z = xr[c] - o.m;
+    yr[c] = LOG ? z - L : expf(z) / o.s;
+  }
+}
+
+template <bool LOG>
+__global__ __launch_bounds__(BS) void sm_bwd_loop_k(const float* __restrict__ y, const float* __restrict__ g,
+                                                    float* __restrict__ dx, int64_t rows, int H) {
+  __shared__ float lds[BS / 64];
+  const int64_t row = blockIdx.x;
+  const float* yr = y + row * H;
+  const float* gr = g + row * H;
+  float s = 0.f;
+  for (int c = threadIdx.x; c < H; c += BS) s += LOG ? gr[c] : gr[c] * yr[c];
+  s = group_sum<BS, float>(s, lds);
+  float* d = dx + row * H;
+  for (int c = threadIdx.x; c < H; c += BS) d[c] = LOG ? gr[c] - expf(yr[c]) * s : yr[c] * (gr[c] - s);
+}
+
+// ---------------------------------------------------------------------------
+// Middle-dim kernels (inner > 1): one thread per (o, i) column.
+
+template <bool LOG>
+__global__ __launch_bounds__(BS) void sm_fwd_col_k(const float* __restrict__ x, float* __restrict__ y,
+                                                   int64_t outer, int64_t len, int64_t inner) {
+  const int64_t id = (int64_t)blockIdx.x * BS + threadIdx.x;
+  if (id >= outer * inner) return;
+  const int64_t o = id / inner, i = id % inner;
+  const float* xc = x + o * len * inner + i;
+  float* yc = y + o * len * inner + i;
+  Online st;
+  for (int64_t k = 0; k < len; ++k) st.add1(xc[k * inner]);
+  const float L = logf(st.s);
+  for (int64_t k = 0; k < len; ++k) {
+    const float z = xc[k * inner] - st.m;
+    yc[k * inner] = LOG ? z - L : expf(z) / st.s;
+  }
+}
+
+template <bool LOG>
+__global__ __launch_bounds__(BS) void sm_bwd_col_k(const float* __restrict__ y, const float* __restrict__ g,
+                                                   float* __restrict__ dx, int64_t outer, int64_t len, int64_t inner) {
+  const int64_t id = (int64_t)blockIdx.x * BS + threadIdx.x;
+  if (id >= outer * inner) return;
+  const int64_t o = id / inner, i = id % inner;
+  const int64_t base = o * len * inner + i;
+  float s = 0.f;
+  for (int64_t k = 0; k < len; ++k) {
+    const int64_t p = base + k * inner;
+    s += LOG ? g[p] : g[p] * y[p];
+  }
+  for (int64_t k = 0; k < len; ++k) {
+    const int64_t p = base + k * inner;
+    dx[p] = LOG ? g[p] - expf(y[p]) * s : y[p] * (g[p] - s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Cross-entropy.
+
+constexpr int CE_BS = 256;
+constexpr int CE_U = 4;  // float4 loads in flight per thread per step
+
+// One block per row. lse[row] = max + log(sum exp(x - max));
+// picked[row] = (x[t] - max) - log(sum)  (the reference's ls[row, t]).
+__global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+                                                  float* __restrict__ lse, float* __restrict__ picked, int64_t n, int C,
+                                                  int vec, int* __restrict__ guard) {
+  __shared__ float lds[2 * (CE_BS / 64)];
+  const int64_t row = blockIdx.x;
+  const float* xr = logits + row * C;
+  Online o;
+  if (vec) {
+    const f4* p = reinterpret_cast<const f4*>(xr);
+    const int c4 = C >> 2;
+    int c = threadIdx.x;
+    for (; c + (CE_U - 1) * CE_BS < c4; c += CE_U * CE_BS) {
+      f4 v[CE_U];
+#pragma unroll
+      for (int u = 0; u < CE_U; ++u) v[u] = __builtin_nontemporal_load(p + c + u * CE_BS);
+      float cm = max4(v[0]);
+#pragma unroll
+      for (int u = 1; u < CE_U; ++u) cm = fmaxf(cm, max4(v[u]));
+      if (cm > o.m) {
+        o.s = (o.m == NEG_INF) ? 0.f : o.s * expf(o.m - cm);
+        o.m = cm;
+      }
+      if (o.m != NEG_INF) {
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < CE_U; ++u) acc += sum4(exp4(v[u] - o.m));
+        o.s += acc;
+      } else {
+#pragma unroll
+        for (int u = 0; u < CE_U; ++u) o.add4(v[u]);
+      }
+    }
+    for (; c < c4; c += CE_BS) o.add4(p[c]);
+  } else {
+    for (int c = threadIdx.x; c < C; c += CE_BS) o.add1(xr[c]);
+  }
+  group_online<CE_BS>(o, lds);
+  if (threadIdx.x == 0) {
+    int64_t t = targets[row];
+    if (t < 0 || t >= C) {
+      atomicOr(guard, 1);
+      t = 0;
+    }
+    const float L = logf(o.s);
+    lse[row] = o.m + L;
+    picked[row] = (xr[t] - o.m) - L;
+  }
+}
+
+// loss[0] = -(sum(picked) / n), sum in float64 in fixed order.
+__global__ __launch_bounds__(1024) void ce_mean_k(const float* __restrict__ picked, int64_t n, float* __restrict__ loss) {
+  __shared__ double s[1024];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) acc += (double)picked[i];
+  s[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 512; w >= 1; w >>= 1) {
+    if ((int)threadIdx.x < w) s[threadIdx.x] += s[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss[0] = -((float)s[0] / (float)n);
+}
+
+// dlogits = (exp(x - lse) - onehot) * (g / n). Grid: (column blocks, rows).
+__global__ __launch_bounds__(CE_BS) void ce_bwd_k(const float* __restrict__ logits, const int64_t* __restrict__ targets,
+                                                  const float* __restrict__ lse, const float* __restrict__ gloss,
+                                                  float* __restrict__ dlogits, int64_t n, int C, int vec) {
+  const int64_t row = blockIdx.y;
+  const float scale = gloss[0] / (float)n;
+  const float l = lse[row];
+  int64_t t = targets[row];
+  const float* xr = logits + row * C;
+  float* dr = dlogits + row * C;
+  if (vec) {
+    const f4* p = reinterpret_cast<const f4*>(xr);
+    f4* q = reinterpret_cast<f4*>(dr);
+    const int c4 = C >> 2;
+    const int per_block = CE_BS * CE_U;
+    const int c0 = blockIdx.x * per_block + threadIdx.x;
+    f4 v[CE_U];
+#pragma unroll
+    for (int u = 0; u < CE_U; ++u) {
+      const int c = c0 + u * CE_BS;
+      if (c < c4) v[u] = __builtin_nontemporal_load(p + c);
+    }
+#pragma unroll
+    for (int u = 0; u < CE_U; ++u) {
+      const int c = c0 + u * CE_BS;
+      if (c < c4) {
+        f4 e = exp4(v[u] - l);
+        const int64_t base = (int64_t)c * 4;
+        if (t >= base && t < base + 4) {
+          const int j = (int)(t - base);
+          if (j == 0) e.x -= 1.f;
+          else if (j == 1) e.y -= 1.f;
+          else if (j == 2) e.z -= 1.f;
+          else e.w -= 1.f;
+        }
+        __builtin_nontemporal_store(e * scale, q + c);
+      }
+    }
+  } else {
+    const int per_block = CE_BS * CE_U;
+    const int c0 = blockIdx.x * per_block + threadIdx.x;
+    for (int u = 0; u < CE_U; ++u) {
+      const int c = c0 + u * CE_BS;
+      if (c < C) {
+        float e = expf(xr[c] - l);
+        if (c == t) e -= 1.f;
+        dr[c] = e * scale;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+
+int pick_cfg(int64_t h4) {
+  if (h4 <= 64) return 641;
+  if (h4 <= 128) return 642;
+  if (h4 <= 192) return 643;
+  if (h4 <= 256) return 644;
+  if (h4 <= 512) return 2562;
+  if (h4 <= 1024) return 2564;
+  if (h4 <= 2048) return 2568;
+  return 0;
+}
+
+bool aligned16(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (reinterpret_cast<uintptr_t>(p) & 15u) return false;
+  return true;
+}
+
+int check_olen(const char* what, int64_t outer, int64_t len, int64_t inner, std::initializer_list<const void*> ps) {
+  if (outer < 0 || len < 0 || inner < 0)
+    return fail(OXI_INVALID_ARGUMENT, "%s: negative size", what);
+  if (len > ((int64_t)1 << 30) || outer * inner > ((int64_t)1 << 40))
+    return fail(OXI_INVALID_ARGUMENT, "%s: size exceeds the kernel limits", what);
+  if (outer && len && inner)
+    for (const void* p : ps)
+      if (!p) return fail(OXI_INVALID_ARGUMENT, "%s: NULL tensor pointer", what);
+  return OXI_OK;
+}
+
+template <bool LOG>
+int launch_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inner) {
+  hipStream_t s = stream();
+  if (inner == 1) {
+    const int cfg = (len % 4 == 0 && aligned16({x, y})) ? pick_cfg(len / 4) : 0;
+    const int h = (int)len;
+#define OXI_SMF(TPR, NV)                                                                                  \
+  case TPR * 10 + NV:                                                                                     \
+    sm_fwd_k<TPR, NV, LOG><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(x, y, outer, h); \
+    break;
+    switch (cfg) {
+      OXI_SMF(64, 1)
+      OXI_SMF(64, 2)
+      OXI_SMF(64, 3)
+      OXI_SMF(64, 4)
+      OXI_SMF(256, 2)
+      OXI_SMF(256, 4)
+      OXI_SMF(256, 8)
+      default:
+        sm_fwd_loop_k<LOG><<<dim3((unsigned)outer), dim3(BS), 0, s>>>(x, y, outer, h);
+    }
+#undef OXI_SMF
+  } else {
+    sm_fwd_col_k<LOG><<<dim3((unsigned)ceil_div(outer * inner, BS)), dim3(BS), 0, s>>>(x, y, outer, len, inner);
+  }
+  return check_launch(LOG ? "log_softmax_fwd" : "softmax_fwd");
+}
+
+template <bool LOG>
+int launch_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t len, int64_t inner) {
+  hipStream_t s = stream();
+  if (inner == 1) {
+    const int cfg = (len % 4 == 0 && aligned16({y, g, dx})) ? pick_cfg(len / 4) : 0;
+    const int h = (int)len;
+#define OXI_SMB(TPR, NV)                                                                                        \
+  case TPR * 10 + NV:                                                                                           \
+    sm_bwd_k<TPR, NV, LOG><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(y, g, dx, outer, h); \
+    break;
+    switch (cfg) {
+      OXI_SMB(64, 1)
+      OXI_SMB(64, 2)
+      OXI_SMB(64, 3)
+      OXI_SMB(64, 4)
+      OXI_SMB(256, 2)
+      OXI_SMB(256, 4)
+      OXI_SMB(256, 8)
+      default:
+        sm_bwd_loop_k<LOG><<<dim3((unsigned)outer), dim3(BS), 0, s>>>(y, g, dx, outer, h);
+    }
+#undef OXI_SMB
+  } else {
+    sm_bwd_col_k<LOG><<<dim3((unsigned)ceil_div(outer * inner, BS)), dim3(BS), 0, s>>>(y, g, dx, outer, len, inner);
+  }
+  return check_launch(LOG ? "log_softmax_bwd" : "softmax_bwd");
+}
+
+}  // namespace
+}  // namespace oxi
+
+using namespace oxi;
+
+extern "C" {
+
+int oxi_softmax_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inner) {
+  if (int rc = check_olen("softmax_fwd", outer, len, inner, {x, y})) return rc;
+  if (outer == 0 || inner == 0 || len == 0) return OXI_OK;
+  OXI_CHECK_INIT();
+  return launch_fwd<false>(x, y, outer, len, inner);
+}
+
+int oxi_softmax_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t len, int64_t inner) {
+  if (int rc = check_olen("softmax_bwd", outer, len, inner, {y, g, dx})) return rc;
+  if (outer == 0 || inner == 0 || len == 0) return OXI_OK;
+  OXI_CHECK_INIT();
+  return launch_bwd<false>(y, g, dx, outer, len, inner);
+}
+
+int oxi_log_softmax_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inner) {
+  if (int rc = check_olen("log_softmax_fwd", outer, len, inner, {x, y})) return rc;
+  if (outer == 0 || inner == 0 || len == 0) return OXI_OK;
+  OXI_CHECK_INIT();
+  return launch_fwd<true>(x, y, outer, len, inner);
+}
+
+int oxi_log_softmax_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t len, int64_t inner) {
+  if (int rc = check_olen("log_softmax_bwd", outer, len, inner, {y, g, dx})) return rc;
+  if (outer == 0 || inner == 0 || len == 0) return OXI_OK;
+  OXI_CHECK_INIT();
+  return launch_bwd<true>(y, g, dx, outer, len, inner);
+}
+
+int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets, float* loss, float* lse, int64_t n, int64_t c) {
+  if (n < 0 || c < 0) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: negative size");
+  if (!loss) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: loss must not be NULL");
+  if (c > ((int64_t)1 << 30) || n > ((int64_t)1 << 31) - 1)
+    return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: size exceeds the kernel limits");
+  OXI_CHECK_INIT();
+  if (n == 0) return oxi_fill(loss, 1, __builtin_nanf(""));  // mean of nothing (Tensor::mean_all, lib.rs:589-593)
+  if (c == 0) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: zero classes");
+  if (!logits || !targets || !lse) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: NULL tensor pointer");
+  Workspace picked(sizeof(float) * (size_t)n);
+  if (!picked.p) return OXI_OTHER;
+  const int vec = (c % 4 == 0 && aligned16({logits})) ? 1 : 0;
+  ce_fwd_k<<<dim3((unsigned)n), dim3(CE_BS), 0, stream()>>>(logits, targets, lse, picked.as<float>(), n, (int)c, vec,
+                                                            guard_flag());
+  if (int rc = check_launch("cross_entropy_fwd")) return rc;
+  ce_mean_k<<<1, 1024, 0, stream()>>>(picked.as<float>(), n, loss);
+  return check_launch("cross_entropy_mean");
+}
+
+int oxi_cross_entropy_bwd(const float* logits, const int64_t* targets, const float* lse, const float* gloss,
+                          float* dlogits, int64_t n, int64_t c) {
+  if (n < 0 || c < 0) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_bwd: negative size");
+  if (c > ((int64_t)1 << 30) || n > 65535LL * 32768LL)
+    return fail(OXI_INVALID_ARGUMENT, "cross_entropy_bwd: size exceeds the kernel limits");
+  if (n == 0 || c == 0) return OXI_OK;
+  if (!logits || !targets || !lse || !gloss || !dlogits)
+    return fail(OXI_INVALID_ARGUMENT, "cross_entropy_bwd: NULL tensor pointer");
+  OXI_CHECK_INIT();
+  const int vec = (c % 4 == 0 && aligned16({logits, dlogits})) ? 1 : 0;
+  const int64_t units = vec ? c / 4 : c;
+  const unsigned gx = (unsigned)ceil_div(units, CE_BS * CE_U);
+  if (n > 65535) {
+    // grid.y is limited; launch row slabs
+    for (int64_t r0 = 0; r0 < n; r0 += 65535) {
+      const int64_t nr = (n - r0) < 65535 ? (n - r0) : 65535;
+      ce_bwd_k<<<dim3(gx, (unsigned)nr), dim3(CE_BS), 0, stream()>>>(logits + r0 * c, targets + r0, lse + r0, gloss,
+                                                                     dlogits + r0 * c, n, (int)c, vec);
+      if (int rc = check_launch("cross_entropy_bwd")) return rc;
+    }
+    return OXI_OK;
+  }
+  ce_bwd_k<<<dim3(gx, (unsigned)n), dim3(CE_BS), 0, stream()>>>(logits, targets, lse, gloss, dlogits, n, (int)c, vec);
+  return check_launch("cross_entropy_bwd");
+}
+
+}  // extern "C"

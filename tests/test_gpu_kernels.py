@@ -1,0 +1,426 @@
+"""Kernel-level parity: liboxihip (through its C-ABI) vs the CPU oracle.
+
+Every test here runs the MI355X kernels and compares them with oracle.ref
+(the f32 restatement of the reference CPU path) and, for long reductions and
+functions the reference lacks, with oracle.closed_form (float64).
+Tolerances are the north-star's: bit-exact for gathers/argmax, otherwise
+rtol 1e-5 / atol 1e-6 in fp32.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, assert_close_arb, assert_reduction_close, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def D(hip, a):
+    return hip.DeviceArray.from_numpy(np.ascontiguousarray(a))
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+
+@pytest.mark.parametrize("shape", [(4096, 768), (7, 33), (64, 1000), (3, 5, 256), (2, 8196), (1, 4096)])
+def test_rms_norm_fwd_bwd_ref(hip, shape):
+    from oracle import ref, closed_form
+    say("rms_norm", shape)
+    r = rng(1)
+    x = r.standard_normal(shape, dtype=np.float32)
+    w = (r.standard_normal(shape[-1], dtype=np.float32) * 0.02 + 1).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    y, rstd = hip.rms_norm_fwd(D(hip, x), D(hip, w), 1e-6)
+    y_ref, inv_ref = ref.rms_norm_fwd(x, w, 1e-6)
+    assert_close(y.numpy(), y_ref, what="rms y")
+    assert_close(rstd.numpy(), inv_ref, what="rms rstd")
+    dx, dw = hip.rms_norm_bwd(D(hip, x), D(hip, w), rstd, D(hip, g), mode="ref")
+    dx_ref, dw_ref = ref.rms_norm_bwd(x, w, inv_ref, g)
+    assert_close(dx.numpy(), dx_ref, what="rms dx(ref)")
+    _, dw64 = closed_form.rms_norm_bwd_refgraph(x, w, g, 1e-6)
+    assert_reduction_close(dw.numpy(), dw_ref, dw64, what="rms dw")
+
+
+@pytest.mark.parametrize("shape", [(4096, 768), (9, 40), (5, 3000)])
+def test_rms_norm_bwd_exact(hip, shape):
+    from oracle import closed_form
+    say("rms_norm exact", shape)
+    r = rng(2)
+    x = r.standard_normal(shape, dtype=np.float32)
+    w = (r.standard_normal(shape[-1], dtype=np.float32) * 0.02 + 1).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    _, rstd = hip.rms_norm_fwd(D(hip, x), D(hip, w), 1e-6)
+    dx, dw = hip.rms_norm_bwd(D(hip, x), D(hip, w), rstd, D(hip, g), mode="exact")
+    dx64, dw64 = closed_form.rms_norm_bwd_exact(x, w, g, 1e-6)
+    assert_close(dx.numpy(), dx64, what="rms dx(exact)")
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm
+
+@pytest.mark.parametrize("shape", [(512, 4096), (16, 768), (7, 33), (6, 1002), (3, 9000), (2, 3, 64)])
+def test_layer_norm_fwd_bwd_ref(hip, shape):
+    from oracle import ref, closed_form
+    say("layer_norm", shape)
+    r = rng(3)
+    x = r.standard_normal(shape, dtype=np.float32)
+    H = shape[-1]
+    w = (r.standard_normal(H, dtype=np.float32) * 0.02 + 1).astype(np.float32)
+    b = (r.standard_normal(H, dtype=np.float32) * 0.02).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    y, mean, rstd = hip.layer_norm_fwd(D(hip, x), D(hip, w), D(hip, b), 1e-5)
+    y_ref, mu_ref, inv_ref = ref.layer_norm_fwd(x, w, b, 1e-5)
+    assert_close(y.numpy(), y_ref, what="ln y")
+    assert_close(mean.numpy(), mu_ref, what="ln mean")
+    assert_close(rstd.numpy(), inv_ref, what="ln rstd")
+    dx, dw, db = hip.layer_norm_bwd(D(hip, x), D(hip, w), mean, rstd, D(hip, g), mode="ref")
+    dx_ref, dw_ref, db_ref = ref.layer_norm_bwd(x, w, mu_ref, inv_ref, g)
+    assert_close(dx.numpy(), dx_ref, what="ln dx(ref)")
+    _, dw64, db64 = closed_form.layer_norm_bwd_refgraph(x, w, g, 1e-5)
+    assert_reduction_close(dw.numpy(), dw_ref, dw64, what="ln dw")
+    assert_reduction_close(db.numpy(), db_ref, db64, what="ln db")
+
+
+@pytest.mark.parametrize("shape", [(512, 4096), (5, 33), (4, 768)])
+def test_layer_norm_bwd_exact(hip, shape):
+    from oracle import closed_form
+    say("layer_norm exact", shape)
+    r = rng(4)
+    x = r.standard_normal(shape, dtype=np.float32)
+    H = shape[-1]
+    w = (r.standard_normal(H, dtype=np.float32) * 0.02 + 1).astype(np.float32)
+    b = (r.standard_normal(H, dtype=np.float32) * 0.02).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    _, mean, rstd = hip.layer_norm_fwd(D(hip, x), D(hip, w), D(hip, b), 1e-5)
+    dx, _, _ = hip.layer_norm_bwd(D(hip, x), D(hip, w), mean, rstd, D(hip, g), mode="exact")
+    dx64, _, _ = closed_form.layer_norm_bwd_exact(x, w, g, 1e-5)
+    assert_close(dx.numpy(), dx64, what="ln dx(exact)")
+
+
+def test_layer_norm_c2_full(hip):
+    """Config 2 at full size: LN(affine) -> exact-erf GELU, forward + backward."""
+    from oracle import ref, closed_form
+    say("layer_norm+gelu C2 (16384, 4096)")
+    r = rng(2)
+    shape = (16384, 4096)
+    x = r.standard_normal(shape, dtype=np.float32)
+    w = (r.standard_normal(4096, dtype=np.float32) * 0.02 + 1).astype(np.float32)
+    b = (r.standard_normal(4096, dtype=np.float32) * 0.02).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    dxx, dw_, db_ = D(hip, x), D(hip, w), D(hip, b)
+    h, mean, rstd = hip.layer_norm_fwd(dxx, dw_, db_, 1e-5)
+    y = hip.gelu_fwd(h, "none")
+    dh = hip.gelu_bwd(h, D(hip, g), "none")
+    dx, dw, db = hip.layer_norm_bwd(dxx, dw_, mean, rstd, dh, mode="ref")
+    h_ref, mu_ref, inv_ref = ref.layer_norm_fwd(x, w, b, 1e-5)
+    hh = h.numpy()
+    assert_close(hh, h_ref, what="C2 h")
+    assert_close(y.numpy(), closed_form.gelu_erf(hh), what="C2 gelu(h)")
+    dh_np = dh.numpy()
+    assert_close(dh_np, closed_form.gelu_erf_grad(hh) * g, what="C2 gelu'(h)*g")
+    dx_ref, dw_ref, db_ref = ref.layer_norm_bwd(x, w, mu_ref, inv_ref, dh_np)
+    assert_close(dx.numpy(), dx_ref, what="C2 dx")
+    _, dw64, db64 = closed_form.layer_norm_bwd_refgraph(x, w, dh_np, 1e-5)
+    assert_reduction_close(dw.numpy(), dw_ref, dw64, what="C2 dw")
+    assert_reduction_close(db.numpy(), db_ref, db64, what="C2 db")
+
+
+# ---------------------------------------------------------------------------
+# Activations
+
+@pytest.mark.parametrize("n", [4, 1, 1023, 1 << 20])
+def test_gelu_tanh(hip, n):
+    from oracle import ref, closed_form
+    say("gelu tanh", n)
+    r = rng(5)
+    x = (r.standard_normal(n, dtype=np.float32) * 3).astype(np.float32)
+    g = r.standard_normal(n, dtype=np.float32)
+    y = hip.gelu_fwd(D(hip, x), "tanh").numpy()
+    assert_close(y, ref.gelu_tanh_fwd(x), what="gelu tanh fwd vs ref")
+    assert_close(y, closed_form.gelu_tanh(x), rtol=1e-5, atol=2e-6, what="gelu tanh fwd vs f64")
+    d = hip.gelu_bwd(D(hip, x), D(hip, g), "tanh").numpy()
+    assert_close(d, ref.gelu_tanh_bwd(x, g), what="gelu tanh bwd vs ref")
+
+
+@pytest.mark.parametrize("n", [5, 4096, 1 << 20])
+def test_gelu_erf(hip, n):
+    from oracle import closed_form
+    say("gelu erf", n)
+    r = rng(6)
+    x = (r.standard_normal(n, dtype=np.float32) * 3).astype(np.float32)
+    g = r.standard_normal(n, dtype=np.float32)
+    assert_close(hip.gelu_fwd(D(hip, x), "none").numpy(), closed_form.gelu_erf(x), what="gelu erf fwd")
+    assert_close(hip.gelu_bwd(D(hip, x), D(hip, g), "none").numpy(), closed_form.gelu_erf_grad(x) * g,
+                 what="gelu erf bwd")
+
+
+def test_silu_contiguous(hip):
+    from oracle import ref
+    say("silu contiguous")
+    r = rng(7)
+    x = (r.standard_normal(100003, dtype=np.float32) * 4).astype(np.float32)
+    g = r.standard_normal(100003, dtype=np.float32)
+    assert_close(hip.silu_fwd(D(hip, x)).numpy(), ref.silu_fwd(x), what="silu fwd")
+    assert_close(hip.silu_bwd(D(hip, x), D(hip, g)).numpy(), ref.silu_bwd(x, g), what="silu bwd")
+
+
+@pytest.mark.parametrize("B,T,H", [(16, 1024, 768), (2, 70, 33)])
+def test_silu_on_transposed_view(hip, B, T, H):
+    """silu(h.permute([0,2,1])): the input is a transposed view (LDS-tiled path)."""
+    from oracle import ref
+    say("silu transposed", (B, T, H))
+    r = rng(8)
+    h = r.standard_normal((B, T, H), dtype=np.float32)
+    view_shape = (B, H, T)
+    view_strides = (T * H, 1, H)  # h.permute([0,2,1])
+    y = hip.silu_fwd(D(hip, h), x_strides=view_strides, shape=view_shape).numpy()
+    hp = np.ascontiguousarray(h.transpose(0, 2, 1))
+    assert_close(y, ref.silu_fwd(hp), what="silu(view)")
+    gview = r.standard_normal(view_shape, dtype=np.float32)
+    d = hip.silu_bwd(D(hip, h), D(hip, gview), x_strides=view_strides, shape=view_shape).numpy()
+    assert_close(d, ref.silu_bwd(hp, gview), what="silu bwd(view)")
+
+
+# ---------------------------------------------------------------------------
+# Softmax family
+
+@pytest.mark.parametrize("shape,dim", [((16384, 768), -1), ((7, 33), -1), ((3, 4, 5), 1), ((2, 9000), -1),
+                                       ((5, 1000), 0), ((64, 4096), -1)])
+def test_softmax_log_softmax(hip, shape, dim):
+    from oracle import ref, closed_form
+    say("softmax", shape, dim)
+    r = rng(9)
+    x = (r.standard_normal(shape, dtype=np.float32) * 2).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    y = hip.softmax_fwd(D(hip, x), dim).numpy()
+    assert_close(y, ref.softmax_fwd(x, dim), what="softmax")
+    assert_close(y, closed_form.softmax(x, dim), what="softmax vs f64")
+    d = hip.softmax_bwd(D(hip, y), D(hip, g), dim).numpy()
+    assert_close_arb(d, ref.softmax_bwd(x, g, dim), closed_form.softmax_bwd(x, g, dim), what="softmax bwd")
+    ly = hip.softmax_fwd(D(hip, x), dim, log=True).numpy()
+    assert_close(ly, ref.log_softmax_fwd(x, dim), what="log_softmax")
+    ld = hip.softmax_bwd(D(hip, ly), D(hip, g), dim, log=True).numpy()
+    assert_close_arb(ld, ref.log_softmax_bwd(x, g, dim), closed_form.log_softmax_bwd(x, g, dim),
+                     what="log_softmax bwd")
+
+
+def test_softmax_kat_and_stability(hip):
+    """Known answers of python/tests/test_nn.py:30-48."""
+    say("softmax KAT")
+    x = np.array([[1.0, 2.0, 3.0], [3.0, 1.0, 2.0]], np.float32)
+    sm = hip.softmax_fwd(D(hip, x)).numpy()
+    ref = np.exp(x) / np.exp(x).sum(-1, keepdims=True)
+    assert np.allclose(sm, ref, atol=1e-6)
+    big = np.array([[1000.0, 1001.0, 1002.0]], np.float32)
+    ls = hip.softmax_fwd(D(hip, big), log=True).numpy()
+    assert np.all(np.isfinite(ls))
+    want = np.exp(np.array([1000.0, 1001.0, 1002.0]) - 1002.0)
+    assert np.allclose(np.exp(ls) / np.exp(ls).sum(), want / want.sum(), atol=1e-6)
+
+
+@pytest.mark.parametrize("n,c", [(2, 3), (64, 1000), (33, 31), (256, 32000)])
+def test_cross_entropy(hip, n, c):
+    from oracle import ref, closed_form
+    say("cross_entropy", n, c)
+    r = rng(10)
+    logits = (r.standard_normal((n, c), dtype=np.float32) * 2).astype(np.float32)
+    t = r.integers(0, c, n).astype(np.int64)
+    loss, lse = hip.cross_entropy_fwd(D(hip, logits), D(hip, t))
+    l = float(loss.numpy()[0])
+    assert abs(l - ref.cross_entropy_fwd(logits, t)) <= 1e-5 * abs(l) + 1e-6
+    assert abs(l - closed_form.cross_entropy(logits, t)) <= 1e-5 * abs(l) + 1e-6
+    gl = D(hip, np.array([1.0], np.float32))
+    d = hip.cross_entropy_bwd(D(hip, logits), D(hip, t), lse, gl).numpy()
+    # dlogits are O(1/n): compare n * dlogits (the 1e-6 abs bound is vacuous otherwise)
+    assert_close_arb(d * n, ref.cross_entropy_bwd(logits, t) * n, closed_form.cross_entropy_grad(logits, t) * n,
+                     what="n*dlogits")
+
+
+def test_cross_entropy_c3_full(hip):
+    """Config 3 at full size (8192, 32000): loss vs float64 over all rows, grads on a row sample."""
+    from oracle import ref, closed_form
+    say("cross_entropy C3 (8192, 32000)")
+    r = rng(3)
+    n, c = 8192, 32000
+    logits = (r.standard_normal((n, c), dtype=np.float32) * 2).astype(np.float32)
+    t = r.integers(0, c, n).astype(np.int64)
+    dl, dt = D(hip, logits), D(hip, t)
+    loss, lse = hip.cross_entropy_fwd(dl, dt)
+    d = hip.cross_entropy_bwd(dl, dt, lse, D(hip, np.array([1.0], np.float32)))
+    l = float(loss.numpy()[0])
+    # float64 loss in row chunks
+    tot = 0.0
+    for s in range(0, n, 1024):
+        ls = closed_form.log_softmax(logits[s:s + 1024])
+        tot += ls[np.arange(ls.shape[0]), t[s:s + 1024]].sum()
+    assert abs(l - (-tot / n)) <= 1e-5 * abs(l)
+    rows = np.sort(r.choice(n, 64, replace=False))
+    dd = d.numpy()[rows]
+    want = ref.cross_entropy_bwd(logits[rows], t[rows]) * len(rows)
+    exact = closed_form.cross_entropy_grad(logits[rows], t[rows]) * len(rows)
+    assert_close_arb(dd * n, want, exact, what="C3 n*dlogits (sampled rows)")
+    assert np.allclose(lse.numpy()[rows],
+                       np.log(np.exp(logits[rows].astype(np.float64)).sum(-1)), rtol=1e-6, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# Gather / embedding
+
+def test_index_select_kats(hip):
+    """python/tests/test_smoke.py:147-149 and test_indexing_grad.py:72-89."""
+    from oracle import ref
+    say("index_select KAT")
+    a = rng(11).standard_normal((4, 6)).astype(np.float32)
+    got = hip.index_select(D(hip, a), 0, D(hip, np.array([3, 0, 2], np.int64))).numpy()
+    np.testing.assert_array_equal(got, a[[3, 0, 2]])
+    got = hip.index_select(D(hip, a), 1, D(hip, np.array([-1, -2], np.int64))).numpy()
+    np.testing.assert_array_equal(got, a[:, [-1, -2]])
+    g = np.array([[1.0, 10.0], [2.0, 20.0], [3.0, 30.0]], np.float32)
+    w = hip.index_select_bwd(D(hip, g), (3, 2), 0, D(hip, np.array([1, 1, 2], np.int64))).numpy()
+    np.testing.assert_array_equal(w, [[0.0, 0.0], [3.0, 30.0], [3.0, 30.0]])
+    g = np.arange(1, 13, dtype=np.float32).reshape(4, 3)
+    w = hip.embedding_bwd(D(hip, g), D(hip, np.array([2, 2, 0, 2], np.int64)), 4).numpy()
+    want = np.zeros((4, 3), np.float32)
+    want[2] = [1 + 4 + 10, 2 + 5 + 11, 3 + 6 + 12]
+    want[0] = [7, 8, 9]
+    np.testing.assert_array_equal(w, want)
+    np.testing.assert_array_equal(ref.index_select_bwd(g, (4, 3), 0, [2, 2, 0, 2]), want)
+
+
+@pytest.mark.parametrize("shape,dim,n", [((50, 8), 0, 200), ((3, 40, 5), 1, 77), ((6, 7), 1, 9),
+                                         ((1000, 129), 0, 3000)])
+def test_index_select_general(hip, shape, dim, n):
+    from oracle import ref
+    say("index_select general", shape, dim, n)
+    r = rng(12)
+    a = r.standard_normal(shape).astype(np.float32)
+    L = shape[dim]
+    idx = r.integers(-L, L, n).astype(np.int64)
+    got = hip.index_select(D(hip, a), dim, D(hip, idx)).numpy()
+    np.testing.assert_array_equal(got, ref.index_select(a, dim, idx))
+    out_shape = list(shape)
+    out_shape[dim] = n
+    g = r.standard_normal(out_shape).astype(np.float32)
+    grad = hip.index_select_bwd(D(hip, g), shape, dim, D(hip, idx)).numpy()
+    np.testing.assert_allclose(grad, ref.index_select_bwd(g, shape, dim, idx), rtol=1e-6, atol=1e-6)
+
+
+def _zipf_ids(seed, shape, V):
+    r = rng(seed)
+    return np.minimum(r.zipf(1.1, shape) - 1, V - 1).astype(np.int64)
+
+
+def test_embedding_c4_full(hip):
+    """Config 4: W (50257, 1024), clipped-Zipf ids (64, 2048): forward bit-exact, dW vs oracle/f64."""
+    from oracle import ref, closed_form
+    say("embedding C4")
+    r = rng(4)
+    V, Dm = 50257, 1024
+    W = r.standard_normal((V, Dm), dtype=np.float32)
+    ids = np.minimum(r.zipf(1.1, (64, 2048)) - 1, V - 1).astype(np.int64).ravel()
+    g = r.standard_normal((ids.size, Dm), dtype=np.float32)
+    dW_, dids = D(hip, W), D(hip, ids)
+    out = hip.embedding_fwd(dW_, dids).numpy()
+    np.testing.assert_array_equal(out, W[ids])
+    dg = D(hip, g)
+    dW = hip.embedding_bwd(dg, dids, V).numpy()
+    dW2 = hip.embedding_bwd(dg, dids, V).numpy()
+    np.testing.assert_array_equal(dW, dW2)  # deterministic, bitwise
+    want32 = ref.index_select_bwd(g, (V, Dm), 0, ids)
+    counts = np.bincount(ids, minlength=V)
+    short = counts <= 64  # single-chunk keys: same position-order f32 sum as the reference
+    np.testing.assert_array_equal(dW[short], want32[short])
+    heavy = np.flatnonzero(~short)
+    exact = np.zeros((heavy.size, Dm))
+    for j, v in enumerate(heavy):
+        exact[j] = g[ids == v].astype(np.float64).sum(0)
+    assert_reduction_close(dW[heavy], want32[heavy], exact, what="C4 heavy dW rows")
+    # conservation: sum over rows of dW equals the sum of all upstream rows
+    assert np.allclose(dW.astype(np.float64).sum(0), g.astype(np.float64).sum(0), rtol=1e-5, atol=1e-3)
+
+
+def test_embedding_out_of_range_guard(hip):
+    say("embedding guard")
+    W = np.ones((5, 4), np.float32)
+    ids = np.array([0, 7], np.int64)  # 7 escaped host validation
+    out = hip.embedding_fwd(D(hip, W), D(hip, ids))
+    with pytest.raises(RuntimeError, match="outside its valid range"):
+        hip.sync()
+    np.testing.assert_array_equal(out.numpy()[1], 0.0)
+    hip.sync()  # the flag was cleared
+
+
+# ---------------------------------------------------------------------------
+# Reductions and the elementwise registry
+
+@pytest.mark.parametrize("kind", ["sum", "mean", "max", "min", "argmax", "argmin", "norm"])
+@pytest.mark.parametrize("shape,dim", [((3, 4, 5), 0), ((3, 4, 5), 1), ((3, 4, 5), 2), ((64, 300), 1),
+                                       ((300, 64), 0), ((16, 8, 768), 0)])
+def test_reduce(hip, kind, shape, dim):
+    from oracle import ref
+    say("reduce", kind, shape, dim)
+    x = rng(13).standard_normal(shape).astype(np.float32)
+    got = hip.reduce(kind, D(hip, x), dim).numpy()
+    want = ref.reduce(kind, x, dim)
+    if kind.startswith("arg"):
+        np.testing.assert_array_equal(got, want)
+    else:
+        assert_close(got, want, rtol=2e-5, what=f"reduce {kind}")
+
+
+def test_reduce_semantics_nan_ties(hip):
+    """First-tie argmax (crates/oxi-tensor/src/tests.rs:188-196), NaN rules of reduce_strip."""
+    say("reduce NaN/ties")
+    x = np.array([[5, 7, 7], [np.nan, 1, 2], [1, np.nan, 3], [np.nan, np.nan, np.nan]] + [[2, 2, 2]] * 60, np.float32)
+    am = hip.reduce("argmax", D(hip, x), 1).numpy()
+    assert list(am[:5]) == [1, 0, 2, 0, 0]
+    mx = hip.reduce("max", D(hip, x), 1).numpy()
+    assert mx[1] == 2 and mx[2] == 3 and mx[3] == -np.inf
+    xt = np.ascontiguousarray(np.tile(np.array([5, 7, 7, 1], np.float32), (64, 1)))
+    np.testing.assert_array_equal(hip.reduce("argmax", D(hip, xt), 1).numpy(), 1)
+
+
+@pytest.mark.parametrize("name", ["neg", "abs", "sqrt", "rsqrt", "exp", "log", "log2", "log10", "sin", "cos",
+                                  "tanh", "relu", "sigmoid", "floor", "ceil", "round", "sign", "square",
+                                  "reciprocal"])
+def test_unary_registry(hip, name):
+    from oracle import ref
+    say("unary", name)
+    a = rng(14).standard_normal((37, 129)).astype(np.float32)
+    if name in ("sqrt", "rsqrt", "log", "log2", "log10", "reciprocal"):
+        a = np.abs(a) + 0.5
+    got = hip.unary(name, D(hip, a)).numpy()
+    assert_close(got, ref.unary(name, a), rtol=2e-6, atol=1e-6, what=name)
+
+
+@pytest.mark.parametrize("name", ["add", "sub", "mul", "div", "pow", "min", "max", "eq", "ne", "lt", "le", "gt",
+                                  "ge"])
+def test_binary_registry_broadcast(hip, name):
+    from oracle import ref
+    say("binary", name)
+    r = rng(15)
+    a = r.standard_normal((3, 70, 129)).astype(np.float32)
+    b = r.standard_normal((70, 1)).astype(np.float32)
+    if name == "pow":
+        a = np.abs(a) + 0.1
+    shape = (3, 70, 129)
+    got = hip.binary(name, D(hip, a), D(hip, b), (70 * 129, 129, 1), (0, 1, 0), shape).numpy()
+    assert_close(got, ref.binary(name, a, b), rtol=2e-6, what=name)
+
+
+def test_binary_transposed_plus_broadcast(hip):
+    """C5's residual add: s.permute([0,2,1]) + pos, pos (1, T, H) broadcast over batch."""
+    say("binary transposed + broadcast")
+    r = rng(16)
+    B, T, H = 4, 130, 96
+    s = r.standard_normal((B, H, T)).astype(np.float32)
+    pos = r.standard_normal((1, T, H)).astype(np.float32)
+    got = hip.binary("add", D(hip, s), D(hip, pos), (H * T, 1, T), (0, H, 1), (B, T, H)).numpy()
+    np.testing.assert_array_equal(got, s.transpose(0, 2, 1) + pos)
