@@ -1,0 +1,221 @@
+// Host core of oxitorch_amd: the C++ restatement of the reference's Rust
+// tensor engine (crates/oxi-tensor), autograd graph (crates/oxi-autograd) and
+// error convention (crates/oxi-core), with a device storage variant whose
+// compute is dispatched through the liboxihip C-ABI (include/oxihip.h).
+//
+// Storage is Host or Device (HIP) behind a refcounted handle; views share it.
+// Every compute op runs on the device; host tensors only stage data
+// (from/to numpy, .cpu()). There is no CPU compute fallback.
+#pragma once
+
+#include <cstdint>
+#include <functional>
+#include <memory>
+#include <mutex>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "oxihip.h"
+
+namespace oxt {
+
+// ---- errors (crates/oxi-core/src/lib.rs:186-211) ---------------------------
+
+enum class ErrKind : int { InvalidArgument = 1, ShapeMismatch = 2, NotImplemented = 3, OutOfBounds = 4, Other = 5 };
+
+class Error : public std::exception {
+ public:
+  Error(ErrKind k, std::string msg) : kind_(k), msg_(std::move(msg)) {}
+  const char* what() const noexcept override { return msg_.c_str(); }
+  ErrKind kind() const { return kind_; }
+
+ private:
+  ErrKind kind_;
+  std::string msg_;
+};
+
+// Display formats of OxitorchError.
+[[noreturn]] void err_invalid(const std::string& m);                      // "invalid argument: m"
+[[noreturn]] void err_shape(const std::string& l, const std::string& r);  // "shape mismatch: l vs r"
+[[noreturn]] void err_notimpl(const std::string& m);                      // "not implemented: m"
+[[noreturn]] void err_oob(const std::string& m);                          // "out of bounds: m"
+[[noreturn]] void err_other(const std::string& m);                        // "m"
+// Raises the Error matching an oxi_status, with liboxihip's message.
+void hip_check(int rc);
+
+// ---- shapes (crates/oxi-tensor/src/layout.rs) -----------------------------
+
+using Shape = std::vector<int64_t>;
+std::string fmt_shape(const Shape& s);  // Rust Debug of a Vec: "[2, 3]"
+Shape row_major_strides(const Shape& s);
+int64_t element_count(const Shape& s);
+Shape validate_shape(const std::vector<int64_t>& dims);
+Shape broadcast_shapes(const Shape& a, const Shape& b);
+Shape broadcast_strides(const Shape& shape, const Shape& strides, const Shape& out);
+int normalize_dim(int64_t dim, int ndim);
+
+// ---- storage + tensor (crates/oxi-tensor/src/lib.rs:24-58) ------------------
+
+enum class Dev { Cpu, Hip };
+Dev default_device();
+void set_default_device(Dev d);
+std::string dev_name(Dev d);
+
+struct Storage {
+  Dev dev;
+  void* ptr = nullptr;
+  size_t nbytes = 0;
+  Storage(Dev d, size_t bytes);
+  ~Storage();
+  Storage(const Storage&) = delete;
+  Storage& operator=(const Storage&) = delete;
+};
+
+class Tensor {
+ public:
+  std::shared_ptr<Storage> st;
+  int64_t offset = 0;  // in elements
+  Shape shape;
+  Shape strides;
+
+  int64_t numel() const { return element_count(shape); }
+  int ndim() const { return (int)shape.size(); }
+  bool is_contiguous() const { return strides == row_major_strides(shape); }
+  Dev dev() const { return st ? st->dev : default_device(); }
+  float* data() const { return st ? static_cast<float*>(st->ptr) + offset : nullptr; }
+
+  static Tensor empty(const Shape& shape, Dev d);
+  static Tensor with_strides(std::shared_ptr<Storage> st, int64_t offset, Shape shape, Shape strides);
+};
+
+// Raises NotImplemented for a host tensor reaching device compute.
+void require_hip(const Tensor& t, const char* what);
+
+// ---- constructors and transfers -----------------------------------------------
+
+Tensor t_full(const Shape& shape, float v, Dev d);         // dense fill (Tensor::full)
+Tensor t_zeros(const Shape& shape, Dev d);
+Tensor t_ones_like(const Tensor& t);
+// A constant of `shape` backed by one element with zero strides: the value of
+// the reference's full-tensor scalar promotion (bindings lib.rs:86-89) without
+// an E-sized fill.
+Tensor t_scalar_full(const Shape& shape, float v, Dev d);
+Tensor t_from_host(const float* data, const Shape& shape, Dev d);
+std::vector<float> t_to_host(const Tensor& t);  // row-major values
+Tensor t_to(const Tensor& t, Dev d);
+
+// ---- views (lib.rs:620-825) --------------------------------------------------
+
+Tensor t_reshape(const Tensor& t, const std::vector<int64_t>& new_shape);
+Tensor t_permute(const Tensor& t, const std::vector<int64_t>& order);
+Tensor t_transpose(const Tensor& t);
+Tensor t_broadcast_to(const Tensor& t, const Shape& out_shape);
+Tensor t_narrow(const Tensor& t, int64_t dim, int64_t lo, int64_t hi, int64_t by);
+Tensor t_select(const Tensor& t, int64_t dim, int64_t index);
+Tensor t_contiguous(const Tensor& t);
+
+// ---- device dispatch (lib.rs:263-357, 478-576, 665-703) ------------------------
+
+int unary_id(const std::string& name);   // InvalidArgument for unknown names
+int binary_id(const std::string& name);
+int cmp_id(const std::string& name);
+Tensor t_unary(int op, const Tensor& a, bool preserve_layout = false);
+Tensor t_binary(int op, const Tensor& a, const Tensor& b, bool preserve_layout = false);
+Tensor t_unary_op(const std::string& name, const Tensor& a);
+Tensor t_binary_op(const std::string& name, const Tensor& a, const Tensor& b);
+Tensor t_cmp_op(const std::string& name, const Tensor& a, const Tensor& b);
+Tensor t_add(const Tensor& a, const Tensor& b);
+Tensor t_mul_scalar(const Tensor& a, float c);
+
+enum class Reduce : int { Sum = 0, Mean, Max, Min, ArgMax, ArgMin, Norm };
+Tensor t_reduce(Reduce kind, const Tensor& t, int64_t dim, bool keepdim);
+// Full reduction to a 0-d tensor (reduce_strip over all elements).
+Tensor t_reduce_all(Reduce kind, const Tensor& t);
+// Validates all indices first (negative wrap); OutOfBounds with the reference text.
+std::vector<int64_t> resolve_indices(const std::vector<int64_t>& idx, int64_t len, int dim);
+Tensor t_index_select(const Tensor& t, int64_t dim, const std::vector<int64_t>& indices);
+// Copies `src` into the (possibly strided) view `dst` of the same shape.
+void t_copy_into(const Tensor& dst, const Tensor& src);
+
+// Strides for an elementwise result: the operands' common dense layout when
+// they all share one (keeps a permuted gradient permuted), else row-major.
+Shape result_strides(const Shape& shape, const std::vector<const Tensor*>& ins);
+// A device int64 buffer holding `v` (kept alive by the returned storage).
+std::shared_ptr<Storage> device_i64(const std::vector<int64_t>& v);
+
+// ---- autograd graph (crates/oxi-autograd/src/graph.rs) ------------------------
+
+bool is_grad_enabled();
+bool set_grad_enabled(bool on);  // returns the previous mode
+
+class Var;
+// A VJP gets the upstream gradient and which inputs need a gradient; it
+// returns one optional gradient per input (unset = not needed / none).
+using Vjp = std::function<std::vector<std::optional<Tensor>>(const Tensor& g, const std::vector<bool>& needs)>;
+
+struct Node {
+  Tensor value;
+  const char* op = nullptr;
+  std::vector<Var> inputs;
+  std::mutex mu;
+  std::optional<Vjp> vjp;
+  std::optional<Tensor> grad;
+  bool requires_grad = false;
+};
+
+class Var {
+ public:
+  std::shared_ptr<Node> node;
+
+  static Var leaf(Tensor value, bool requires_grad);
+  static Var op(Tensor value, const char* name, std::vector<Var> inputs, Vjp vjp);
+  const Tensor& value() const { return node->value; }
+  bool requires_grad() const { return node->requires_grad; }
+  const char* op_name() const { return node->op; }
+  std::optional<Tensor> grad() const;
+  void set_grad(const Tensor& g) const;
+  void zero_grad() const;
+  void accumulate_grad(const Tensor& g) const;
+};
+
+Tensor unbroadcast(const Tensor& g, const Shape& shape);
+void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph);
+
+// ---- differentiable ops (crates/oxi-autograd/src/ops.rs) ------------------------
+
+namespace aops {
+Var add(const Var& a, const Var& b);
+Var sub(const Var& a, const Var& b);
+Var mul(const Var& a, const Var& b);
+Var div(const Var& a, const Var& b);
+Var pow(const Var& a, const Var& b);
+Var neg(const Var& x);
+Var abs(const Var& x);
+Var exp(const Var& x);
+Var log(const Var& x);
+Var sqrt(const Var& x);
+Var tanh(const Var& x);
+Var sigmoid(const Var& x);
+Var relu(const Var& x);
+Var reduce(const Var& x, Reduce kind, int64_t dim, bool keepdim);
+Var reshape(const Var& x, const std::vector<int64_t>& shape);
+Var permute(const Var& x, const std::vector<int64_t>& order);
+Var transpose(const Var& x);
+Var broadcast_to(const Var& x, const Shape& shape);
+Var narrow(const Var& x, int64_t dim, int64_t lo, int64_t hi, int64_t by);
+Var index_select(const Var& x, int64_t dim, const std::vector<int64_t>& indices);
+
+// Fused hot-path nodes: one graph node and one kernel per direction.
+enum class NormVjp { Ref = OXI_NORM_VJP_REF, Exact = OXI_NORM_VJP_EXACT };
+NormVjp norm_vjp_mode();  // OXI_NORM_VJP=ref|exact (default ref)
+Var rms_norm(const Var& x, const Var& w, float eps, NormVjp mode);
+Var layer_norm(const Var& x, const std::optional<Var>& w, const std::optional<Var>& b, float eps, NormVjp mode);
+Var gelu(const Var& x, int approximate);
+Var silu(const Var& x);
+Var softmax(const Var& x, int64_t dim, bool log);
+Var cross_entropy(const Var& logits, const std::vector<int64_t>& targets);
+Var embedding(const std::vector<int64_t>& indices, const Var& weight);
+}  // namespace aops
+
+}  // namespace oxt

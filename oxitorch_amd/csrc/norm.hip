@@ -281,9 +281,13 @@ __global__ __launch_bounds__(BS) void norm_bwd_loop_k(const float* __restrict__ 
 }
 
 // out[c] = sum over partial rows b (fixed order, float64) of part[b][c].
+// A block owns 64 columns; its FIN_W waves each sum the rows b = s, s+FIN_W,
+// ... of one slice s, then the slice sums are added in slice order.
 // blockIdx.y selects the dw (0) or db (1) plane.
-__global__ __launch_bounds__(256) void col_finish_k(const float* __restrict__ part, int nb, int H,
-                                                    float* __restrict__ out0, float* __restrict__ out1) {
+constexpr int FIN_W = 16;
+
+__global__ __launch_bounds__(64 * FIN_W) void col_finish_k(const float* __restrict__ part, int nb, int H,
+                                                           float* __restrict__ out0, float* __restrict__ out1) {
   float* out = blockIdx.y ? out1 : out0;
   if (!out) return;
   const float* p = part + (int64_t)blockIdx.y * nb * H;
@@ -291,12 +295,19 @@ __global__ __launch_bounds__(256) void col_finish_k(const float* __restrict__ pa
   const int slice = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
   double acc = 0.0;
-  if (c < H)
-    for (int b = slice; b < nb; b += 4) acc += (double)p[(int64_t)b * H + c];
-  __shared__ double s[4][64];
+  if (c < H) {
+#pragma unroll 4
+    for (int b = slice; b < nb; b += FIN_W) acc += (double)p[(int64_t)b * H + c];
+  }
+  __shared__ double s[FIN_W][64];
   s[slice][lane] = acc;
   __syncthreads();
-  if (slice == 0 && c < H) out[c] = (float)(((s[0][lane] + s[1][lane]) + s[2][lane]) + s[3][lane]);
+  if (slice == 0 && c < H) {
+    double t = s[0][lane];
+#pragma unroll
+    for (int i = 1; i < FIN_W; ++i) t += s[i][lane];
+    out[c] = (float)t;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -387,7 +398,7 @@ int launch_bwd(const float* x, const float* w, const float* mean, const float* r
   int rc = check_launch(LN ? "layer_norm_bwd" : "rms_norm_bwd");
   if (rc != OXI_OK) return rc;
   if (need_part) {
-    col_finish_k<<<dim3((unsigned)ceil_div(H, 64), LN ? 2 : 1), dim3(256), 0, s>>>(part, (int)nblk, h, dw,
+    col_finish_k<<<dim3((unsigned)ceil_div(H, 64), LN ? 2 : 1), dim3(64 * FIN_W), 0, s>>>(part, (int)nblk, h, dw,
                                                                                     LN ? db : nullptr);
     rc = check_launch("norm_param_grad_finish");
   }

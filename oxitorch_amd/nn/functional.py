@@ -1,0 +1,132 @@
+"""Functional API of the hot path, same signatures as the reference
+python/oxitorch/nn/functional.py:182-293.
+
+Where the reference composes each F.* from several graph ops, this module
+calls one fused device node (one kernel forward, one kernel backward), whose
+values and gradients match the composition within the parity tolerances.
+Inputs the fused nodes do not take (a weight that is not a (H,) vector,
+for instance) fall back to the reference's composition of graph ops, still
+on the device.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .. import _native
+
+
+def _native_from_numpy(arr, requires_grad=False):
+    """Build a graph-connected tensor from a numpy array (default device)."""
+    return _native.from_numpy(np.ascontiguousarray(arr, dtype=np.float32), requires_grad)
+
+
+# ---- activations (functional.py:182-208) ---------------------------------------
+
+def relu(x):
+    return x.apply("relu")
+
+
+def sigmoid(x):
+    return x.apply("sigmoid")
+
+
+def tanh(x):
+    return x.apply("tanh")
+
+
+def gelu(x, approximate="tanh"):
+    """GELU. `approximate='tanh'` is the reference's F.gelu
+    0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))); `'none'` is the exact
+    0.5 x (1 + erf(x / sqrt 2)), which the reference does not have."""
+    return _native.gelu(x, approximate)
+
+
+def silu(x):
+    """SiLU / swish: `x * sigmoid(x)`."""
+    return _native.silu(x)
+
+
+def leaky_relu(x, negative_slope=0.01):
+    return x.apply("relu") + (x * float(negative_slope)).apply("neg").apply("relu").apply("neg")
+
+
+# ---- softmax family (functional.py:211-222) -------------------------------------
+
+def softmax(x, dim=-1):
+    """Numerically stable softmax along `dim`."""
+    return _native.softmax(x, dim)
+
+
+def log_softmax(x, dim=-1):
+    """`log_softmax = x - max - log(sum(exp(x - max)))`, stable."""
+    return _native.log_softmax(x, dim)
+
+
+# ---- normalization (functional.py:227-240) ----------------------------------------
+
+def _is_vec(t, H):
+    return t is not None and len(t.shape) == 1 and t.shape[0] == H
+
+
+def layer_norm(x, weight, bias, eps=1e-5, vjp=None):
+    """LayerNorm over the last dim with affine `weight`/`bias`.
+
+    `vjp` selects the x-gradient: "ref" (default, or OXI_NORM_VJP) reproduces
+    the reference graph, where `.apply("rsqrt")` detaches the inverse std;
+    "exact" is the full derivative."""
+    H = x.shape[-1]
+    if _is_vec(weight, H) and _is_vec(bias, H):
+        return _native.layer_norm(x, weight, bias, eps, vjp)
+    mu = x.mean(-1, True)
+    centered = x - mu
+    var = (centered * centered).mean(-1, True)
+    inv = (var + float(eps)).apply("rsqrt")
+    return centered * inv * weight + bias
+
+
+def rms_norm(x, weight, eps=1e-6, vjp=None):
+    """RMSNorm over the last dim: `x / rms(x) * weight` (`vjp` as in layer_norm)."""
+    if _is_vec(weight, x.shape[-1]):
+        return _native.rms_norm(x, weight, eps, vjp)
+    ms = (x * x).mean(-1, True)
+    inv = (ms + float(eps)).apply("rsqrt")
+    return x * inv * weight
+
+
+# ---- embedding (functional.py:245-247) -----------------------------------------------
+
+def embedding(indices, weight):
+    """`weight` is `(num_embeddings, dim)`; `indices` is a flat sequence of ints."""
+    idx = np.asarray(indices, dtype=np.int64).ravel().tolist()
+    return _native.embedding(idx, weight)
+
+
+# ---- losses (functional.py:270-293) -----------------------------------------------------
+
+def mse_loss(pred, target):
+    diff = pred - target
+    return (diff * diff).mean()
+
+
+def cross_entropy(logits, targets):
+    """Mean cross-entropy; `targets` is a flat list of int class indices.
+
+    Fused: one streaming pass forward (per-row log-sum-exp and the picked
+    log-probability), one backward writing (softmax - onehot) * g / n. The
+    argument checks mirror the reference's: a batch-size mismatch raises
+    ValueError mentioning the targets, and class ids follow numpy indexing
+    (negatives wrap, out-of-range raises IndexError)."""
+    n, classes = logits.shape
+    t = np.asarray(targets, dtype=np.int64).ravel()
+    if len(t) != n:
+        raise ValueError(f"{len(t)} targets for batch of {n}")
+    bad = (t >= classes) | (t < -classes)
+    if bad.any():
+        raise IndexError(f"index {int(t[bad][0])} is out of bounds for axis 1 with size {classes}")
+    t = np.where(t < 0, t + classes, t)
+    return _native.cross_entropy(logits, t.tolist())
+
+
+def linear(*args, **kwargs):
+    raise NotImplementedError("linear (SGEMM) is outside this build's device hot path")
