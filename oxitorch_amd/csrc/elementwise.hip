@@ -204,6 +204,81 @@ __global__ __launch_bounds__(BS) void map_tiled_k(F f, Plan<N> p, int jd, unsign
   }
 }
 
+// tiled, float4 flavour: same 64x64 tiles, every global access a 16-byte
+// vector (4 consecutive elements along the transposed input's unit-stride
+// dim when loading, along the output's innermost dim when storing).
+template <class F, int N>
+__global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, unsigned tmask, int64_t tiles_d,
+                                                      int64_t tiles_j) {
+  __shared__ float tile[N][T][T + 1];
+  const int d = p.ndim - 1;
+  int64_t b = blockIdx.x;
+  const int64_t td = b % tiles_d;
+  b /= tiles_d;
+  const int64_t tj = b % tiles_j;
+  b /= tiles_j;
+  int64_t off[N + 1];
+#pragma unroll
+  for (int k = 0; k <= N; ++k) off[k] = 0;
+  for (int q = p.ndim - 2; q >= 0; --q) {
+    if (q == jd) continue;
+    const int64_t c = b % p.shape[q];
+    b /= p.shape[q];
+#pragma unroll
+    for (int k = 0; k <= N; ++k) off[k] += c * p.st[k][q];
+  }
+  const int64_t j0 = tj * T, d0 = td * T;
+  const int64_t nj = p.shape[jd], nd = p.shape[d];
+  const int t = threadIdx.x;
+  // loads of transposed inputs: 16 lanes cover 64 consecutive j of one d
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    if (!(tmask >> k & 1u)) continue;
+    const float* q = p.x[k] + off[k + 1];
+#pragma unroll
+    for (int i = 0; i < (T * T / 4) / BS; ++i) {
+      const int l = i * BS + t;
+      const int jj = (l % (T / 4)) * 4, dd = l / (T / 4);
+      const int64_t gj = j0 + jj, gd = d0 + dd;
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (gj < nj && gd < nd) v = *reinterpret_cast<const f4*>(q + gj + gd * p.st[k + 1][d]);
+      tile[k][dd][jj] = v.x;
+      tile[k][dd][jj + 1] = v.y;
+      tile[k][dd][jj + 2] = v.z;
+      tile[k][dd][jj + 3] = v.w;
+    }
+  }
+  __syncthreads();
+  // compute + store: 16 lanes cover 64 consecutive d of one j
+#pragma unroll
+  for (int i = 0; i < (T * T / 4) / BS; ++i) {
+    const int l = i * BS + t;
+    const int dd = (l % (T / 4)) * 4, jj = l / (T / 4);
+    const int64_t gj = j0 + jj, gd = d0 + dd;
+    if (gj >= nj || gd >= nd) continue;
+    f4 in[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      if (tmask >> k & 1u) {
+        in[k] = f4{tile[k][dd][jj], tile[k][dd + 1][jj], tile[k][dd + 2][jj], tile[k][dd + 3][jj]};
+      } else {
+        const float* q = p.x[k] + off[k + 1] + gj * p.st[k + 1][jd];
+        if (p.st[k + 1][d] == 0) in[k] = f4{q[0], q[0], q[0], q[0]};
+        else in[k] = *reinterpret_cast<const f4*>(q + gd);
+      }
+    }
+    f4 r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float v[N];
+#pragma unroll
+      for (int k = 0; k < N; ++k) v[k] = in[k][c];
+      r[c] = apply<F, N>(f, v);
+    }
+    __builtin_nontemporal_store(r, reinterpret_cast<f4*>(p.y + off[0] + gj * p.st[0][jd] + gd));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // generic: one element per thread, full index arithmetic.
 
@@ -382,7 +457,24 @@ int launch_map(F f, const char* what, float* y, const int64_t* ys, const float* 
       const int64_t batch = n / (p.shape[d] * p.shape[jd]);
       const int64_t blocks = tiles_d * tiles_j * batch;
       if (blocks < ((int64_t)1 << 31)) {
-        map_tiled_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
+        // 16-byte accesses need 4-element alignment of every row start touched
+        bool vec = p.shape[d] % 4 == 0 && p.shape[jd] % 4 == 0 && al16(p.y);
+        for (int q = 0; q < p.ndim && vec; ++q)
+          if (q != d && p.st[0][q] % 4) vec = false;
+        for (int k = 0; k < N && vec; ++k) {
+          const bool tr = tmask >> k & 1u;
+          if (p.st[k + 1][d] == 0 && !tr) continue;  // broadcast along d: scalar reads
+          if (!al16(p.x[k])) vec = false;
+          for (int q = 0; q < p.ndim && vec; ++q) {
+            if (tr && q == jd) continue;   // the unit-stride dim of a transposed input
+            if (!tr && q == d) continue;   // the unit-stride dim of a direct input
+            if (p.st[k + 1][q] % 4) vec = false;
+          }
+        }
+        if (vec)
+          map_tiled_vec_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
+        else
+          map_tiled_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
         return check_launch(what);
       }
     }

@@ -7,22 +7,24 @@
 // with float4 accesses (8 independent loads in flight per thread).
 //
 // VJP without float atomics:
-//   1. keys: ids wrapped to [0, len) (out-of-range -> sentinel key `len`,
-//      guard flag raised), per-key counts via integer atomics (order-free);
-//   2. one-block scans: key offsets, chunks per key (ceil(count / CH)), and
-//      partial-slot offsets for keys that span several chunks;
-//   3. stable LSD radix sort of positions by key, 8-bit digits: per-tile digit
-//      histograms, a scan, then a wave-synchronous scatter whose ranks come
-//      from ballots, so equal keys keep position order;
-//   4. chunk sums: each chunk of <= CH positions of one key is summed in
-//      position order in f32 (the reference's own order, so keys with
-//      <= CH occurrences are bit-identical to it) and written straight to the
-//      output row, or to a partial slot when the key spans several chunks;
-//   5. finalize: rows of absent keys are zero-filled and multi-chunk keys add
-//      their partial rows in chunk order in float64.
-// Heavy keys (a clipped-Zipf id can own a third of all positions) are split
-// across many chunks, so no single block serialises on them.
+//   1. keys: ids wrapped to [0, len); out-of-range ids get the sentinel key
+//      `len` (never summed) and raise the guard flag;
+//   2. stable LSD radix sort of positions by key, 8-bit digits: per-tile digit
+//      histograms (LDS integer atomics), a one-block LDS scan, and a scatter
+//      whose ranks come from wave ballots plus per-wave counts, so equal keys
+//      keep position order;
+//   3. tile-segmented reduction over the sorted positions: each block owns
+//      ST positions and sums every run of equal keys in position order in
+//      f32 -- the reference's own order, so a run inside one tile gives a
+//      bit-identical row -- writing complete runs straight to the output and
+//      runs cut by a tile edge to per-tile partial slots;
+//   4. fix-up: a key spanning several tiles adds its partial slots in tile
+//      order in float64 (16 waves split the slots, so a key that owns a third
+//      of all positions is not serialised on one wave);
+//   5. rows of absent keys are zero-filled.
+// Every block does the same amount of work whatever the id distribution.
 #include <algorithm>
+#include <type_traits>
 
 #include "internal.h"
 #include "rowtile.h"
@@ -31,8 +33,6 @@ namespace oxi {
 namespace {
 
 constexpr int BS = 256;
-constexpr int CH = 64;        // positions per chunk
-constexpr int TILE = 1024;    // positions per radix tile (one wave per tile)
 constexpr int GRPB = 8;       // rows per gather step
 
 __device__ __forceinline__ int64_t wrap_id(int64_t id, int64_t len, bool& ok) {
@@ -104,93 +104,119 @@ __global__ __launch_bounds__(BS) void gather_elem_k(const float* __restrict__ sr
 }
 
 // ---------------------------------------------------------------------------
-// VJP step 1: keys + per-key counts.
+// VJP step 1: keys. Out-of-range ids become the sentinel key `len` (never
+// summed) and raise the guard flag.
 
 __global__ __launch_bounds__(BS) void keys_k(const int64_t* __restrict__ idx, int64_t n, int64_t len,
-                                             int* __restrict__ keys, int* __restrict__ pos,
-                                             int* __restrict__ counts, int* __restrict__ guard) {
+                                             int* __restrict__ keys, int* __restrict__ pos, int* __restrict__ guard) {
   for (int64_t p = (int64_t)blockIdx.x * BS + threadIdx.x; p < n; p += (int64_t)gridDim.x * BS) {
     bool ok;
     const int64_t id = wrap_id(idx[p], len, ok);
-    const int key = ok ? (int)id : (int)len;
     if (!ok) atomicOr(guard, 1);
-    keys[p] = key;
+    keys[p] = ok ? (int)id : (int)len;
     pos[p] = (int)p;
-    atomicAdd(&counts[key], 1);
-  }
-}
-
-// Exclusive scan of m ints (one block of 1024 threads); `total` gets the sum.
-// `in` may equal `out`: each thread reads and rewrites only its own range.
-__global__ __launch_bounds__(1024) void scan_k(const int* in, int* out, int64_t m, int* total) {
-  __shared__ int s[1024];
-  const int t = threadIdx.x;
-  const int64_t per = (m + 1023) / 1024;
-  const int64_t b = t * per, e = min(b + per, m);
-  int sum = 0;
-  for (int64_t i = b; i < e; ++i) sum += in[i];
-  s[t] = sum;
-  __syncthreads();
-  for (int w = 1; w < 1024; w <<= 1) {
-    const int v = (t >= w) ? s[t - w] : 0;
-    __syncthreads();
-    s[t] += v;
-    __syncthreads();
-  }
-  int run = s[t] - sum;
-  for (int64_t i = b; i < e; ++i) {
-    const int v = in[i];
-    out[i] = run;
-    run += v;
-  }
-  if (t == 1023 && total) *total = s[1023];
-}
-
-// chunks per key and partial slots per multi-chunk key
-__global__ __launch_bounds__(BS) void chunk_counts_k(const int* __restrict__ counts, int64_t len,
-                                                     int* __restrict__ nch, int* __restrict__ npart) {
-  for (int64_t v = (int64_t)blockIdx.x * BS + threadIdx.x; v < len; v += (int64_t)gridDim.x * BS) {
-    const int c = counts[v];
-    const int k = (c + CH - 1) / CH;
-    nch[v] = k;
-    npart[v] = k > 1 ? k : 0;
   }
 }
 
 // ---------------------------------------------------------------------------
-// VJP step 3: stable LSD radix sort (8-bit digits), one wave per tile.
+// VJP step 2: stable LSD radix sort of (key, position), 8-bit digits.
+// A block owns a tile of RT consecutive elements (256 threads x 8 items).
 
+constexpr int RT = 2048;
+
+// hist[d * ntiles + tile] = number of elements of `tile` whose digit is d.
 __global__ __launch_bounds__(BS) void radix_hist_k(const int* __restrict__ keys, int64_t n, int shift, int ntiles,
                                                    int* __restrict__ hist) {
-  __shared__ int cnt[BS / 64][256];
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int tile = blockIdx.x * (BS / 64) + w;
-  for (int d = lane; d < 256; d += 64) cnt[w][d] = 0;
+  __shared__ int cnt[256];
+  const int t = threadIdx.x;
+  cnt[t] = 0;
   __syncthreads();
-  if (tile < ntiles) {
-    for (int i = lane; i < TILE; i += 64) {
-      const int64_t p = (int64_t)tile * TILE + i;
-      if (p < n) atomicAdd(&cnt[w][(keys[p] >> shift) & 255], 1);
-    }
+  const int64_t base = (int64_t)blockIdx.x * RT;
+#pragma unroll
+  for (int i = 0; i < RT / BS; ++i) {
+    const int64_t p = base + i * BS + t;
+    if (p < n) atomicAdd(&cnt[(keys[p] >> shift) & 255], 1);  // LDS integer atomics: exact counts
   }
   __syncthreads();
-  if (tile < ntiles)
-    for (int d = lane; d < 256; d += 64) hist[(int64_t)d * ntiles + tile] = cnt[w][d];
+  hist[(int64_t)t * ntiles + blockIdx.x] = cnt[t];
 }
 
+// In-place exclusive scan of m ints by one block of 1024 threads, in LDS
+// chunks of 8192 (coalesced loads/stores; padded LDS rows avoid bank conflicts).
+constexpr int SCAN_T = 1024;
+constexpr int SCAN_CHUNK = 8 * SCAN_T;
+
+__device__ __forceinline__ int pad_idx(int e) { return e + (e >> 3); }
+
+__global__ __launch_bounds__(SCAN_T) void scan_k(int* a, int64_t m) {
+  __shared__ int buf[SCAN_CHUNK + SCAN_CHUNK / 8];
+  __shared__ int wsum[SCAN_T / 64];
+  __shared__ int carry_s;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  if (t == 0) carry_s = 0;
+  for (int64_t base = 0; base < m; base += SCAN_CHUNK) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = i * SCAN_T + t;
+      buf[pad_idx(e)] = (base + e < m) ? a[base + e] : 0;
+    }
+    __syncthreads();
+    int v[8], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      v[k] = buf[pad_idx(t * 8 + k)];
+      sum += v[k];
+    }
+    // inclusive wave scan of per-thread sums
+    int inc = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(inc, d, 64);
+      if (lane >= d) inc += o;
+    }
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    if (t == 0) {
+      int run = 0;
+      for (int q = 0; q < SCAN_T / 64; ++q) {
+        const int x = wsum[q];
+        wsum[q] = run;
+        run += x;
+      }
+    }
+    __syncthreads();
+    int run = carry_s + wsum[w] + inc - sum;  // exclusive prefix of this thread
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      buf[pad_idx(t * 8 + k)] = run;
+      run += v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = i * SCAN_T + t;
+      if (base + e < m) a[base + e] = buf[pad_idx(e)];
+    }
+    if (t == SCAN_T - 1) carry_s = run;
+    __syncthreads();
+  }
+}
+
+// Stable scatter: element r*256 + t of a tile goes after every earlier element
+// with the same digit. Ranks within a wave come from ballots; counts of the
+// earlier waves of the same round from LDS.
 __global__ __launch_bounds__(BS) void radix_scatter_k(const int* __restrict__ keys, const int* __restrict__ vals,
-                                                      int64_t n, int shift, int ntiles, const int* __restrict__ base_in,
+                                                      int64_t n, int shift, int ntiles, const int* __restrict__ offs,
                                                       int* __restrict__ keys_out, int* __restrict__ vals_out) {
-  __shared__ int base[BS / 64][256];
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int tile = blockIdx.x * (BS / 64) + w;
-  if (tile < ntiles)
-    for (int d = lane; d < 256; d += 64) base[w][d] = base_in[(int64_t)d * ntiles + tile];
-  __syncthreads();
+  __shared__ int base[256];
+  __shared__ int cnt[BS / 64][256];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  base[t] = offs[(int64_t)t * ntiles + blockIdx.x];
   const unsigned long long lt = (1ull << lane) - 1ull;
-  for (int r = 0; r < TILE / 64; ++r) {
-    const int64_t p = (int64_t)tile * TILE + r * 64 + lane;
-    const bool valid = tile < ntiles && p < n;
+  const int64_t tile0 = (int64_t)blockIdx.x * RT;
+  for (int r = 0; r < RT / BS; ++r) {
+    const int64_t p = tile0 + r * BS + t;
+    const bool valid = p < n;
     const int k = valid ? keys[p] : 0;
     const int v = valid ? vals[p] : 0;
     const int d = (k >> shift) & 255;
@@ -201,106 +227,177 @@ __global__ __launch_bounds__(BS) void radix_scatter_k(const int* __restrict__ ke
       const unsigned long long m = __ballot(bit);
       peers &= bit ? m : ~m;
     }
+#pragma unroll
+    for (int q = 0; q < BS / 64; ++q) cnt[q][t] = 0;
+    __syncthreads();
+    if (valid && (__ffsll((long long)peers) - 1) == lane) cnt[w][d] = __popcll(peers);
+    __syncthreads();
     if (valid) {
-      const int dst = base[w][d] + __popcll(peers & lt);
+      int pre = base[d];
+      for (int q = 0; q < w; ++q) pre += cnt[q][d];
+      const int dst = pre + __popcll(peers & lt);
       keys_out[dst] = k;
       vals_out[dst] = v;
     }
-    __syncthreads();  // every lane has read base[] for this round
-    if (valid && (__ffsll((long long)peers) - 1) == lane) base[w][d] += __popcll(peers);
+    __syncthreads();
+    int add = 0;
+#pragma unroll
+    for (int q = 0; q < BS / 64; ++q) add += cnt[q][t];
+    base[t] += add;
     __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------------
-// VJP step 4: chunk sums. Persistent grid; chunk c belongs to the last key v
-// with choff[v] <= c.
+// VJP step 3: tile-segmented reduction. A block owns ST consecutive sorted
+// positions; every run of equal keys inside the tile is summed in position
+// order. A run that neither continues from the previous tile nor into the
+// next one is complete: its sum is the output row. Otherwise the sum goes to
+// a partial slot of the tile: slot 2*tile+1 for the run that continues into
+// the next tile, slot 2*tile for the first run continuing from the previous.
+
+constexpr int ST = 128;
+constexpr int SU = 8;  // rows in flight per thread
 
 template <bool VEC>
-__global__ __launch_bounds__(BS) void chunk_sum_k(const float* __restrict__ g, int64_t outer, int64_t n,
-                                                  int64_t inner, int64_t len, const int* __restrict__ perm,
-                                                  const int* __restrict__ offs, const int* __restrict__ counts,
-                                                  const int* __restrict__ nch, const int* __restrict__ choff,
-                                                  const int* __restrict__ poff, const int* __restrict__ total_chunks,
-                                                  float* __restrict__ grad, float* __restrict__ part) {
-  __shared__ int sh[4];
-  const int total = *total_chunks;
+__global__ __launch_bounds__(BS) void seg_tile_k(const float* __restrict__ g, int64_t outer, int64_t n, int64_t inner,
+                                                 int64_t len, const int* __restrict__ skeys,
+                                                 const int* __restrict__ perm, float* __restrict__ grad,
+                                                 float* __restrict__ part, int* __restrict__ present) {
+  __shared__ int key_s[ST + 2];  // [0] = key before the tile (-1 if none), [cnt+1] = key after
+  __shared__ int pos_s[ST];
+  const int t = threadIdx.x;
+  const int64_t p0 = (int64_t)blockIdx.x * ST;
+  const int cnt = (int)min<int64_t>(ST, n - p0);
+  if (t < cnt) {
+    key_s[t + 1] = skeys[p0 + t];
+    pos_s[t] = perm[p0 + t];
+  }
+  if (t == 0) key_s[0] = p0 > 0 ? skeys[p0 - 1] : -1;
+  if (t == 1) key_s[cnt + 1] = p0 + cnt < n ? skeys[p0 + cnt] : -1;
+  __syncthreads();
+  if (t == 0) {  // mark present keys (plain stores of 1: order-free)
+    for (int i = 0; i < cnt; ++i)
+      if (key_s[i + 1] != key_s[i] && key_s[i + 1] < len) present[key_s[i + 1]] = 1;
+  }
   const int64_t units = VEC ? inner / 4 : inner;
-  for (int c = blockIdx.x; c < total; c += gridDim.x) {
-    if (threadIdx.x == 0) {
-      int lo = 0, hi = (int)len;  // search over keys [0, len) only: the sentinel key is never summed
-      while (lo < hi) {          // first v with choff[v] > c
-        const int mid = (lo + hi) >> 1;
-        if (choff[mid] <= c) lo = mid + 1;
-        else hi = mid;
-      }
-      const int v = lo - 1;
-      const int j = c - choff[v];
-      sh[0] = v;
-      sh[1] = offs[v] + j * CH;
-      sh[2] = min(CH, counts[v] - j * CH);
-      sh[3] = nch[v] == 1 ? -1 : poff[v] + j;
-    }
-    __syncthreads();
-    const int v = sh[0], start = sh[1], cnt = sh[2], slot = sh[3];
-    __syncthreads();
-    for (int64_t o = 0; o < outer; ++o) {
-      const float* gb = g + o * n * inner;
-      float* dst = slot < 0 ? grad + (o * len + v) * inner : part + ((int64_t)slot * outer + o) * inner;
-      for (int64_t u = threadIdx.x; u < units; u += BS) {
-        if constexpr (VEC) {
-          f4 acc = {0.f, 0.f, 0.f, 0.f};
-          int r = 0;
-          for (; r + 8 <= cnt; r += 8) {
-            f4 t[8];
+  const int64_t slot_head = 2 * (int64_t)blockIdx.x, slot_tail = slot_head + 1;
+  for (int64_t o = 0; o < outer; ++o) {
+    const float* gb = g + o * n * inner;
+    for (int64_t u = t; u < units; u += BS) {
+      using V = typename std::conditional<VEC, f4, float>::type;
+      V acc = V{};
+      int start = 0;
+      for (int i = 0; i < cnt; i += SU) {
+        V vals[SU];
 #pragma unroll
-            for (int q = 0; q < 8; ++q) t[q] = reinterpret_cast<const f4*>(gb + (int64_t)perm[start + r + q] * inner)[u];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc = acc + t[q];
+        for (int j = 0; j < SU; ++j) {
+          if (i + j < cnt) {
+            const float* row = gb + (int64_t)pos_s[i + j] * inner;
+            if constexpr (VEC) vals[j] = reinterpret_cast<const f4*>(row)[u];
+            else vals[j] = row[u];
           }
-          for (; r < cnt; ++r) acc = acc + reinterpret_cast<const f4*>(gb + (int64_t)perm[start + r] * inner)[u];
-          __builtin_nontemporal_store(acc, reinterpret_cast<f4*>(dst) + u);
-        } else {
-          float acc = 0.f;
-          for (int r = 0; r < cnt; ++r) acc += gb[(int64_t)perm[start + r] * inner + u];
-          dst[u] = acc;
+        }
+#pragma unroll
+        for (int j = 0; j < SU; ++j) {
+          const int q = i + j;
+          if (q >= cnt) break;
+          acc = acc + vals[j];
+          const int key = key_s[q + 1];
+          if (key_s[q + 2] != key || q == cnt - 1) {  // run [start, q] ends here
+            if (key < len) {
+              const bool head_inc = (start == 0) && (key_s[0] == key);
+              const bool tail_inc = (q == cnt - 1) && (key_s[cnt + 1] == key);
+              float* dst;
+              if (!head_inc && !tail_inc) dst = grad + (o * len + key) * inner;
+              else dst = part + ((tail_inc ? slot_tail : slot_head) * outer + o) * inner;
+              if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
+              else dst[u] = acc;
+            }
+            acc = V{};
+            start = q + 1;
+          }
         }
       }
     }
   }
 }
 
-// VJP step 5: every row (o, v) of grad not written by a single-chunk key.
+// VJP step 4: a segment spanning tiles ta..tb is owned by ta; its partials
+// are the tail slots of ta..tb-1 and the head slot of tb, added in tile order
+// in float64. Block: 16 waves x 64 lanes, blockIdx.y = column chunk.
+constexpr int FX_W = 16;
+
 template <bool VEC>
-__global__ __launch_bounds__(BS) void finalize_k(int64_t outer, int64_t len, int64_t inner,
-                                                 const int* __restrict__ nch, const int* __restrict__ poff,
-                                                 const float* __restrict__ part, float* __restrict__ grad) {
-  const int64_t row = blockIdx.x;  // o * len + v
-  const int64_t v = row % len, o = row / len;
-  const int k = nch[v];
-  if (k == 1) return;
-  float* dst = grad + row * inner;
-  const int64_t units = VEC ? inner / 4 : inner;
-  if (k == 0) {
-    for (int64_t u = threadIdx.x; u < units; u += BS) {
-      if constexpr (VEC) __builtin_nontemporal_store(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + u);
-      else dst[u] = 0.f;
-    }
-    return;
+__global__ __launch_bounds__(64 * FX_W) void seg_fixup_k(int64_t outer, int64_t n, int64_t inner, int64_t len,
+                                                         const int* __restrict__ skeys,
+                                                         const float* __restrict__ part, float* __restrict__ grad) {
+  const int64_t tile = blockIdx.x;
+  const int64_t p0 = tile * ST;
+  const int64_t p1 = min<int64_t>(p0 + ST, n);
+  if (p1 >= n) return;  // nothing continues past the last tile
+  const int klast = skeys[p1 - 1];
+  if (skeys[p1] != klast || klast >= len) return;                       // tail run ends in this tile
+  if (p0 > 0 && skeys[p0] == klast && skeys[p0 - 1] == klast) return;  // run started in an earlier tile
+  // last position of the segment: upper_bound over [p1, n) - 1
+  int64_t lo = p1, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (skeys[mid] <= klast) lo = mid + 1;
+    else hi = mid;
   }
-  const int p0 = poff[v];
-  for (int64_t u = threadIdx.x; u < units; u += BS) {
-    if constexpr (VEC) {
-      double a0 = 0, a1 = 0, a2 = 0, a3 = 0;
-      for (int j = 0; j < k; ++j) {
-        const f4 t = reinterpret_cast<const f4*>(part + ((int64_t)(p0 + j) * outer + o) * inner)[u];
-        a0 += t.x; a1 += t.y; a2 += t.z; a3 += t.w;
+  const int64_t tb = (lo - 1) / ST;
+  const int64_t m = tb - tile + 1;  // partial slots
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t u = (int64_t)blockIdx.y * 64 + lane;
+  const int64_t units = VEC ? inner / 4 : inner;
+  __shared__ double red[FX_W][64][VEC ? 4 : 1];
+  for (int64_t o = 0; o < outer; ++o) {
+    double a[4] = {0.0, 0.0, 0.0, 0.0};
+    if (u < units) {
+      for (int64_t j = wv; j < m; j += FX_W) {
+        const int64_t slot = (j < m - 1) ? 2 * (tile + j) + 1 : 2 * tb;
+        const float* src = part + (slot * outer + o) * inner;
+        if constexpr (VEC) {
+          const f4 v = reinterpret_cast<const f4*>(src)[u];
+          a[0] += v.x; a[1] += v.y; a[2] += v.z; a[3] += v.w;
+        } else {
+          a[0] += src[u];
+        }
       }
-      reinterpret_cast<f4*>(dst)[u] = f4{(float)a0, (float)a1, (float)a2, (float)a3};
-    } else {
-      double a = 0;
-      for (int j = 0; j < k; ++j) a += part[((int64_t)(p0 + j) * outer + o) * inner + u];
-      dst[u] = (float)a;
+    }
+#pragma unroll
+    for (int c = 0; c < (VEC ? 4 : 1); ++c) red[wv][lane][c] = a[c];
+    __syncthreads();
+    if (wv == 0 && u < units) {
+      double r[4] = {0.0, 0.0, 0.0, 0.0};
+      for (int q = 0; q < FX_W; ++q)
+#pragma unroll
+        for (int c = 0; c < (VEC ? 4 : 1); ++c) r[c] += red[q][lane][c];
+      float* dst = grad + (o * len + klast) * inner;
+      if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = f4{(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
+      else dst[u] = (float)r[0];
+    }
+    __syncthreads();
+  }
+}
+
+// VJP step 5: rows of keys that never occur are zero.
+constexpr int ZR = 4;  // rows per block
+
+template <bool VEC>
+__global__ __launch_bounds__(BS) void zero_absent_k(int64_t outer, int64_t len, int64_t inner,
+                                                    const int* __restrict__ present, float* __restrict__ grad) {
+  const int64_t units = VEC ? inner / 4 : inner;
+  for (int r = 0; r < ZR; ++r) {
+    const int64_t v = (int64_t)blockIdx.x * ZR + r;
+    if (v >= len || present[v]) continue;
+    for (int64_t o = 0; o < outer; ++o) {
+      float* dst = grad + (o * len + v) * inner;
+      for (int64_t u = threadIdx.x; u < units; u += BS) {
+        if constexpr (VEC) __builtin_nontemporal_store(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + u);
+        else dst[u] = 0.f;
+      }
     }
   }
 }
@@ -353,69 +450,53 @@ int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inn
   if (n == 0) return oxi_fill(grad, total_out, 0.f);
   if (!g || !idx) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: NULL tensor pointer");
   hipStream_t s = stream();
-  const int64_t nk = len + 1;  // + sentinel key for invalid ids
-  const int ntiles = (int)ceil_div(n, TILE);
+  const int64_t rtiles = ceil_div(n, RT);
+  const int64_t stiles = ceil_div(n, ST);
+  if (rtiles * 256 > ((int64_t)1 << 31) || len + 1 >= ((int64_t)1 << 31))
+    return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many indices");
   int passes = 0;
-  for (int64_t m = len; m > 0; m >>= 8) ++passes;
+  for (int64_t m = len; m > 0; m >>= 8) ++passes;  // keys are in [0, len]
   if (passes == 0) passes = 1;
-  const int64_t max_parts = 2 * ceil_div(n, CH) + 1;
-  // workspace layout (ints): keys, pos, keys2, pos2 (n each); counts, offs, nch, choff, npart, poff (nk each);
-  // hist (256 * ntiles); scalars (4)
-  const size_t ints = 4 * (size_t)n + 6 * (size_t)nk + 256 * (size_t)ntiles + 4;
+  // workspace (ints): keys, pos, keys2, pos2 (n each), hist (256 * rtiles), present (len)
+  const size_t ints = 4 * (size_t)n + 256 * (size_t)rtiles + (size_t)len;
   Workspace wsi(ints * sizeof(int));
-  Workspace wsp((size_t)max_parts * (size_t)outer * (size_t)inner * sizeof(float));
+  Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(float));
   if (!wsi.p || !wsp.p) return OXI_OTHER;
   int* keys = wsi.as<int>();
   int* pos = keys + n;
   int* keys2 = pos + n;
   int* pos2 = keys2 + n;
-  int* counts = pos2 + n;
-  int* offs = counts + nk;
-  int* nch = offs + nk;
-  int* choff = nch + nk;
-  int* npart = choff + nk;
-  int* poff = npart + nk;
-  int* hist = poff + nk;
-  int* scal = hist + 256 * (int64_t)ntiles;  // [0] total chunks, [1] total partial slots, [2] n keys
-  if (int rc = oxi_fill(reinterpret_cast<float*>(counts), nk, 0.f)) return rc;  // +0.0f is all-zero bits
+  int* hist = pos2 + n;
+  int* present = hist + 256 * rtiles;
+  if (int rc = oxi_fill(reinterpret_cast<float*>(present), len, 0.f)) return rc;  // +0.0f is all-zero bits
   const unsigned gb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, BS), (int64_t)cu_count() * 8));
-  keys_k<<<gb, BS, 0, s>>>(idx, n, len, keys, pos, counts, guard_flag());
+  keys_k<<<gb, BS, 0, s>>>(idx, n, len, keys, pos, guard_flag());
   if (int rc = check_launch("index_select_bwd/keys")) return rc;
-  scan_k<<<1, 1024, 0, s>>>(counts, offs, nk, scal + 2);
-  const unsigned gk = (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(len, BS), (int64_t)cu_count() * 8));
-  chunk_counts_k<<<gk, BS, 0, s>>>(counts, len, nch, npart);
-  // the sentinel key contributes no chunks
-  if (int rc = oxi_fill(reinterpret_cast<float*>(nch + len), 1, 0.f)) return rc;
-  if (int rc = oxi_fill(reinterpret_cast<float*>(npart + len), 1, 0.f)) return rc;
-  scan_k<<<1, 1024, 0, s>>>(nch, choff, nk, scal + 0);
-  scan_k<<<1, 1024, 0, s>>>(npart, poff, nk, scal + 1);
-  if (int rc = check_launch("index_select_bwd/scans")) return rc;
-  // radix sort (keys, pos) -> sorted positions
   int *ka = keys, *va = pos, *kb = keys2, *vb = pos2;
-  const unsigned gt = (unsigned)ceil_div(ntiles, BS / 64);
   for (int ps = 0; ps < passes; ++ps) {
     const int shift = 8 * ps;
-    radix_hist_k<<<gt, BS, 0, s>>>(ka, n, shift, ntiles, hist);
-    scan_k<<<1, 1024, 0, s>>>(hist, hist, 256 * (int64_t)ntiles, nullptr);
-    radix_scatter_k<<<gt, BS, 0, s>>>(ka, va, n, shift, ntiles, hist, kb, vb);
+    radix_hist_k<<<(unsigned)rtiles, BS, 0, s>>>(ka, n, shift, (int)rtiles, hist);
+    scan_k<<<1, SCAN_T, 0, s>>>(hist, 256 * rtiles);
+    radix_scatter_k<<<(unsigned)rtiles, BS, 0, s>>>(ka, va, n, shift, (int)rtiles, hist, kb, vb);
     std::swap(ka, kb);
     std::swap(va, vb);
   }
   if (int rc = check_launch("index_select_bwd/sort")) return rc;
-  const bool vec = inner % 4 == 0 && al16(g) && al16(grad) && inner >= 4;
-  const unsigned gc = (unsigned)std::max<int64_t>(
-      1, std::min<int64_t>(ceil_div(n, CH) + std::min<int64_t>(len, n), (int64_t)cu_count() * 8));
+  const bool vec = inner % 4 == 0 && al16(g) && al16(grad);
   float* part = wsp.as<float>();
-  if (vec)
-    chunk_sum_k<true><<<gc, BS, 0, s>>>(g, outer, n, inner, len, va, offs, counts, nch, choff, poff, scal, grad, part);
-  else
-    chunk_sum_k<false><<<gc, BS, 0, s>>>(g, outer, n, inner, len, va, offs, counts, nch, choff, poff, scal, grad, part);
-  if (int rc = check_launch("index_select_bwd/chunks")) return rc;
-  const int64_t frows = outer * len;
-  if (frows >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many output rows");
-  if (vec) finalize_k<true><<<(unsigned)frows, BS, 0, s>>>(outer, len, inner, nch, poff, part, grad);
-  else finalize_k<false><<<(unsigned)frows, BS, 0, s>>>(outer, len, inner, nch, poff, part, grad);
-  return check_launch("index_select_bwd/finalize");
+  if (vec) seg_tile_k<true><<<(unsigned)stiles, BS, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present);
+  else seg_tile_k<false><<<(unsigned)stiles, BS, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present);
+  if (int rc = check_launch("index_select_bwd/segments")) return rc;
+  const int64_t units = vec ? inner / 4 : inner;
+  const dim3 fg((unsigned)stiles, (unsigned)ceil_div(units, 64));
+  if (fg.y > 65535) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: rows too wide");
+  if (vec) seg_fixup_k<true><<<fg, 64 * FX_W, 0, s>>>(outer, n, inner, len, ka, part, grad);
+  else seg_fixup_k<false><<<fg, 64 * FX_W, 0, s>>>(outer, n, inner, len, ka, part, grad);
+  if (int rc = check_launch("index_select_bwd/fixup")) return rc;
+  const unsigned gz = (unsigned)ceil_div(len, ZR);
+  if (vec) zero_absent_k<true><<<gz, BS, 0, s>>>(outer, len, inner, present, grad);
+  else zero_absent_k<false><<<gz, BS, 0, s>>>(outer, len, inner, present, grad);
+  return check_launch("index_select_bwd/zero");
 }
 
 int oxi_embedding_fwd(const float* W, const int64_t* ids, int64_t n, int64_t V, int64_t D, float* out) {

@@ -17,6 +17,7 @@
 #include <algorithm>
 
 #include "internal.h"
+#include "rowtile.h"
 
 namespace oxi {
 namespace {
@@ -79,6 +80,38 @@ __global__ __launch_bounds__(BS) void reduce_strided_k(const float* __restrict__
     a.init(p.len ? s[0] : 0.f);
     for (int64_t k = 0; k < p.len; ++k) a.add(s[k * p.rst], k);
     out[e] = a.result(p.len);
+  }
+}
+
+// Four adjacent outputs per thread when they are adjacent in memory (the
+// last remaining dim has stride 1): 16-byte loads walk the strip. Same
+// sequential fold per output as reduce_strided_k. Not used for arg* kinds.
+template <int K>
+__global__ __launch_bounds__(BS) void reduce_strided_vec_k(const float* __restrict__ x, RPlan p, int64_t nout4,
+                                                           float* __restrict__ out) {
+  for (int64_t e4 = (int64_t)blockIdx.x * BS + threadIdx.x; e4 < nout4; e4 += (int64_t)gridDim.x * BS) {
+    const float* s = x + base_of(p, e4 * 4);
+    f4 a;
+    if constexpr (K == OXI_REDUCE_MAX) a = f4{-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf()};
+    else if constexpr (K == OXI_REDUCE_MIN) a = f4{__builtin_huge_valf(), __builtin_huge_valf(), __builtin_huge_valf(), __builtin_huge_valf()};
+    else a = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int64_t k = 0; k < p.len; ++k) {
+      const f4 v = *reinterpret_cast<const f4*>(s + k * p.rst);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if constexpr (K == OXI_REDUCE_SUM || K == OXI_REDUCE_MEAN) a[c] += v[c];
+        else if constexpr (K == OXI_REDUCE_NORM) a[c] += v[c] * v[c];
+        else if constexpr (K == OXI_REDUCE_MAX) a[c] = fmaxf(a[c], v[c]);
+        else a[c] = fminf(a[c], v[c]);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if constexpr (K == OXI_REDUCE_MEAN) a[c] = a[c] / (float)p.len;
+      else if constexpr (K == OXI_REDUCE_NORM) a[c] = sqrtf(a[c]);
+    }
+    *reinterpret_cast<f4*>(out + e4 * 4) = a;
   }
 }
 
@@ -151,6 +184,19 @@ int launch(const float* x, const RPlan& p, int64_t nout, float* out) {
     const int64_t blocks = ceil_div(nout * 64, BS);
     if (blocks < ((int64_t)1 << 31)) {
       reduce_contig_k<K><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(x, p, nout, out);
+      return check_launch("reduce");
+    }
+  }
+  if constexpr (K != OXI_REDUCE_ARGMAX && K != OXI_REDUCE_ARGMIN) {
+    // vector path: innermost remaining dim contiguous, every row start 16-byte aligned
+    bool vec = p.nd > 0 && p.st[p.nd - 1] == 1 && p.size[p.nd - 1] % 4 == 0 && p.rst % 4 == 0 &&
+               (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+    for (int d = 0; d + 1 < p.nd && vec; ++d)
+      if (p.st[d] % 4) vec = false;
+    if (vec) {
+      const int64_t nout4 = nout / 4;
+      const int64_t blocks = std::min<int64_t>(ceil_div(nout4, BS), (int64_t)cu_count() * 64);
+      reduce_strided_vec_k<K><<<dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(BS), 0, s>>>(x, p, nout4, out);
       return check_launch("reduce");
     }
   }

@@ -75,27 +75,57 @@ def assert_reduction_close(got, ref32, exact64, rtol=RTOL, atol=ATOL, what=""):
 def assert_close_arb(got, ref32, exact64, rtol=RTOL, atol=ATOL, what=""):
     """Parity with the reference path, arbitrated by float64 where they differ.
 
-    An element passes if it is within rtol/atol of the f32 reference path, or
-    within rtol/atol of the float64 closed form, or at least as close to the
-    float64 closed form as the reference path is. The reference's composed
-    softmax-family VJPs add a mathematically-zero max-path term whose f32
-    rounding noise (a sum of O(1) terms over the row) lands on the argmax
-    element; where that noise exceeds the tolerance the arbiter decides.
+    An element passes if it is within rtol/atol of the f32 reference path or of
+    the float64 evaluation. The remaining elements must be no further from the
+    float64 evaluation (in units of the tolerance) than the reference path's own
+    worst element is: the device result is then no less accurate than the path
+    it replaces. Where this matters: the reference's composed softmax-family
+    VJPs add a mathematically-zero max-path term whose f32 rounding noise lands
+    on the argmax element, and long chains of f32 ops round differently in any
+    two evaluation orders.
     """
     got = np.asarray(got, dtype=np.float64)
     ref32 = np.asarray(ref32, dtype=np.float64)
     exact64 = np.asarray(exact64, dtype=np.float64)
     assert got.shape == ref32.shape == exact64.shape, f"{what}: shapes differ"
-    e_ref = np.abs(got - ref32)
-    e_ex = np.abs(got - exact64)
-    ok = (e_ref <= atol + rtol * np.abs(ref32)) | (e_ex <= atol + rtol * np.abs(exact64)) | (
-        e_ex <= np.abs(ref32 - exact64))
-    if not ok.all():
+    tol_ex = atol + rtol * np.abs(exact64)
+    ok = (np.abs(got - ref32) <= atol + rtol * np.abs(ref32)) | (np.abs(got - exact64) <= tol_ex)
+    if ok.all():
+        return
+    worst_got = (np.abs(got - exact64) / tol_ex)[~ok].max()
+    worst_ref = (np.abs(ref32 - exact64) / tol_ex).max()
+    if worst_got > worst_ref:
         i = np.flatnonzero(~ok.ravel())[0]
         raise AssertionError(
-            f"{what}: {(~ok).sum()} of {ok.size} elements fail both the reference and the float64 arbiter; "
-            f"first at flat {i}: got {got.ravel()[i]!r} ref {ref32.ravel()[i]!r} f64 {exact64.ravel()[i]!r}"
-        )
+            f"{what}: {(~ok).sum()} of {ok.size} elements outside both tolerances, worst {worst_got:.3g} x tol "
+            f"from float64 vs the reference path's worst {worst_ref:.3g} x tol; first at flat {i}: got "
+            f"{got.ravel()[i]!r} ref {ref32.ravel()[i]!r} f64 {exact64.ravel()[i]!r}")
+
+
+def assert_sum_close(got, ref32, abs_sum, rtol=RTOL, atol=ATOL, what=""):
+    """Parity for short sums with cancellation: |got - ref| <= atol + rtol * sum|terms|.
+
+    Any f32 evaluation order of a sum has an error bounded by a multiple of
+    eps * sum|terms|; relative to |sum| that bound is unbounded when the
+    terms cancel, so the tolerance is taken relative to the sum's condition.
+    """
+    got = np.asarray(got, dtype=np.float64)
+    ref32 = np.asarray(ref32, dtype=np.float64)
+    abs_sum = np.asarray(abs_sum, dtype=np.float64)
+    err = np.abs(got - ref32)
+    bad = err > atol + rtol * abs_sum
+    assert not bad.any(), f"{what}: {bad.sum()} elements outside rtol*sum|terms|; max err {err.max():.3e}"
+
+
+def segmented_runs_in_one_tile(ids, V, tile=128):
+    """Keys whose stably-sorted run of positions lies inside one `tile`-position
+    block of the embedding VJP: their rows are summed in position order in f32
+    in one pass, exactly as the reference does, so they must match bitwise."""
+    keys = np.where(np.asarray(ids) < 0, np.asarray(ids) + V, np.asarray(ids))
+    counts = np.bincount(keys, minlength=V)
+    start = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    end = start + counts - 1
+    return (counts > 0) & (start // tile == end // tile)
 
 
 def rng(seed):

@@ -9,7 +9,8 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import assert_close, assert_close_arb, assert_reduction_close, rng
+from conftest import (assert_close, assert_close_arb, assert_reduction_close, assert_sum_close, rng,
+                      segmented_runs_in_one_tile)
 
 pytestmark = pytest.mark.gpu
 
@@ -314,9 +315,10 @@ def test_config4_embedding(ox, F):
     out.backward(_t(ox, g))
     dW = W.grad.numpy()
     want = ref.index_select_bwd(g, (V, D), 0, ids)
-    short = np.bincount(ids, minlength=V) <= 64
-    np.testing.assert_array_equal(dW[short], want[short])
-    heavy = np.flatnonzero(~short)
+    counts = np.bincount(ids, minlength=V)
+    one = segmented_runs_in_one_tile(ids, V)
+    np.testing.assert_array_equal(dW[one], want[one])
+    heavy = np.flatnonzero(~one & (counts > 0))
     exact = np.stack([g[ids == v].astype(np.float64).sum(0) for v in heavy])
     assert_reduction_close(dW[heavy], want[heavy], exact, what="C4 heavy rows")
 
@@ -334,6 +336,7 @@ def _c5_oracle(ref, Wa, ids, lnw, lnb, rw, pos, g, softmax_bwd):
     dpos = np.zeros((1, 1024, 768), np.float32)
     for b in range(16):  # unbroadcast: sequential f32 over the batch axis
         dpos[0] = dpos[0] + dr[b]
+    dpos_abs = np.abs(dr.astype(np.float64)).sum(0, keepdims=True)
     ds = np.ascontiguousarray(dr.transpose(0, 2, 1))
     dhp = ref.silu_bwd(hp, ds)
     dh = np.ascontiguousarray(dhp.transpose(0, 2, 1))
@@ -343,7 +346,29 @@ def _c5_oracle(ref, Wa, ids, lnw, lnb, rw, pos, g, softmax_bwd):
     xh = (e.astype(np.float64) - mu.reshape(16, 1024, 1)) * inv.reshape(16, 1024, 1)
     exact = dict(lnw=(dh * xh).reshape(-1, 768).sum(0), lnb=dh.astype(np.float64).reshape(-1, 768).sum(0),
                  rw=(dn.astype(np.float64) * rr * inv2.reshape(16, 1024, 1)).reshape(-1, 768).sum(0))
+    exact["pos_abs"] = dpos_abs
     return y, dict(W=dW, lnw=dlnw, lnb=dlnb, rw=drw, pos=dpos), exact
+
+
+def _c5_f64(Wa, ids, lnw, lnb, rw, pos, g):
+    """The whole C5 chain in float64 closed forms (reference-graph VJPs: the
+    norms' inverse std is detached, as in the reference)."""
+    from oracle import closed_form as cf
+    B, T, H = 16, 1024, 768
+    e = Wa.astype(np.float64)[ids].reshape(B, T, H)
+    h, mu, inv = cf.layer_norm_fwd(e, lnw, lnb, 1e-5)
+    hp = h.transpose(0, 2, 1)
+    s = cf.silu(hp)
+    rr = s.transpose(0, 2, 1) + pos
+    n, inv2 = cf.rms_norm_fwd(rr, rw, 1e-6)
+    y = cf.softmax(n)
+    dn = cf.softmax_bwd(n, g)
+    dr, drw = cf.rms_norm_bwd_refgraph(rr, rw, dn, 1e-6)
+    dpos = dr.sum(0, keepdims=True)
+    dhp = cf.silu_grad(hp) * dr.transpose(0, 2, 1)
+    de, dlnw, dlnb = cf.layer_norm_bwd_refgraph(e, lnw, dhp.transpose(0, 2, 1), 1e-5)
+    dW = cf.embedding_grad(de.reshape(-1, H), ids, Wa.shape[0])
+    return y, dict(W=dW, lnw=dlnw, lnb=dlnb, rw=drw, pos=dpos)
 
 
 def test_config5_gpt2_chain(ox, F):
@@ -362,14 +387,13 @@ def test_config5_gpt2_chain(ox, F):
     assert s.is_contiguous()  # forward outputs are row-major, as the reference's
     y = F.softmax(F.rms_norm(s.permute([0, 2, 1]) + P, RW), -1)
     y.backward(_t(ox, g))
-    from oracle import closed_form
     y_ref, grads, _ = _c5_oracle(ref, Wa, ids, lnw, lnb, rw, pos, g, ref.softmax_bwd)
-    # the same chain with the softmax VJP in float64: free of the reference's
-    # max-path rounding noise, it arbitrates elements where the two differ
-    _, grads64, exact = _c5_oracle(ref, Wa, ids, lnw, lnb, rw, pos, g, closed_form.softmax_bwd)
-    assert_close(y.numpy(), y_ref, what="C5 y")
+    y64, g64 = _c5_f64(Wa, ids, lnw, lnb, rw, pos, g)
+    assert_close_arb(y.numpy(), y_ref, y64, what="C5 y")
     got = dict(W=W.grad.numpy(), lnw=LW.grad.numpy(), lnb=LB.grad.numpy(), rw=RW.grad.numpy(), pos=P.grad.numpy())
-    assert_close_arb(got["pos"], grads["pos"], grads64["pos"], what="C5 pos grad")
-    assert_close_arb(got["W"], grads["W"], grads64["W"], what="C5 dW")
+    # Ten f32 stages each round differently on the device and in the oracle;
+    # where the two differ beyond tolerance the float64 chain arbitrates.
+    for k in ("W", "pos"):
+        assert_close_arb(got[k], grads[k], g64[k], what=f"C5 d{k}")
     for k in ("lnw", "lnb", "rw"):  # column sums over 16384 rows
-        assert_reduction_close(got[k], grads[k], exact[k], what=f"C5 d{k}")
+        assert_reduction_close(got[k], grads[k], g64[k], what=f"C5 d{k}")

@@ -12,7 +12,8 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import assert_close, assert_close_arb, assert_reduction_close, rng
+from conftest import (assert_close, assert_close_arb, assert_reduction_close, rng,
+                      segmented_runs_in_one_tile)
 
 pytestmark = pytest.mark.gpu
 
@@ -335,9 +336,10 @@ def test_embedding_c4_full(hip):
     np.testing.assert_array_equal(dW, dW2)  # deterministic, bitwise
     want32 = ref.index_select_bwd(g, (V, Dm), 0, ids)
     counts = np.bincount(ids, minlength=V)
-    short = counts <= 64  # single-chunk keys: same position-order f32 sum as the reference
-    np.testing.assert_array_equal(dW[short], want32[short])
-    heavy = np.flatnonzero(~short)
+    one = segmented_runs_in_one_tile(ids, V)  # same position-order f32 sum as the reference
+    np.testing.assert_array_equal(dW[one], want32[one])
+    np.testing.assert_array_equal(dW[counts == 0], 0.0)
+    heavy = np.flatnonzero(~one & (counts > 0))
     exact = np.zeros((heavy.size, Dm))
     for j, v in enumerate(heavy):
         exact[j] = g[ids == v].astype(np.float64).sum(0)
