@@ -38,6 +38,13 @@ sys.path.insert(0, ROOT)
 
 METRIC = "achieved HBM GB/s (% of MI355X peak) + rows/s, norm/softmax/embed fwd+bwd"
 
+# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled
+# by the same counters' reading of a 1 GiB copy (FETCH x2.0, WRITE x1.0);
+# the runs and the per-kernel table are in profiles/pmc_traffic_c2.md.
+TRAFFIC_BYTES = {
+    "c2": {"layer_norm_fwd": 538.2e6, "gelu_erf_fwd": 537.0e6, "gelu_erf_bwd": 805.5e6, "layer_norm_bwd": 840.2e6},
+}
+
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
@@ -432,7 +439,9 @@ def main():
         "kernel_ms_per_step": round(kernel_ms, 5),
         "kernels": {k: {"avg_ms": round(v["ms"], 5), "gbs": round(v["gbs"], 1)} for k, v in per.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(d["gbs"] / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(d["gbs"] / PEAK_HBM_GBS, 4),
+                     "traffic": TRAFFIC_BYTES.get(args.config, {}).get(dom),
+                     "algorithmic_bytes": d["bytes"]},
         "cpu_baseline": None,
     }
     if not args.no_copy_probe:

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(BS) void map_flat_vec_k(F f, Plan<N> p, int64_t n, 
 #pragma unroll
     for (int k = 0; k < N; ++k) {
       if (bcast_mask >> k & 1u) in[k][u] = f4{sc[k], sc[k], sc[k], sc[k]};
-      else if (i < n4) in[k][u] = reinterpret_cast<const f4*>(p.x[k])[i];
+      else if (i < n4) in[k][u] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p.x[k]) + i);
     }
   }
 #pragma unroll
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, un
       const int jj = (l % (T / 4)) * 4, dd = l / (T / 4);
       const int64_t gj = j0 + jj, gd = d0 + dd;
       f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (gj < nj && gd < nd) v = *reinterpret_cast<const f4*>(q + gj + gd * p.st[k + 1][d]);
+      if (gj < nj && gd < nd) v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(q + gj + gd * p.st[k + 1][d]));
       tile[k][dd][jj] = v.x;
       tile[k][dd][jj + 1] = v.y;
       tile[k][dd][jj + 2] = v.z;

@@ -294,7 +294,7 @@ __global__ __launch_bounds__(BS) void seg_tile_k(const float* __restrict__ g, in
         for (int j = 0; j < SU; ++j) {
           if (i + j < cnt) {
             const float* row = gb + (int64_t)pos_s[i + j] * inner;
-            if constexpr (VEC) vals[j] = reinterpret_cast<const f4*>(row)[u];
+            if constexpr (VEC) vals[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(row) + u);
             else vals[j] = row[u];
           }
         }
