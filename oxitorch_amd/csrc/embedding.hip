@@ -6,23 +6,22 @@
 // Gather: out[o, k, :] = src[o, idx[k], :]. Each block copies 8 rows per step
 // with float4 accesses (8 independent loads in flight per thread).
 //
-// VJP without float atomics:
-//   1. keys: ids wrapped to [0, len); out-of-range ids get the sentinel key
-//      `len` (never summed) and raise the guard flag;
-//   2. stable LSD radix sort of positions by key, 8-bit digits: per-tile digit
-//      histograms (LDS integer atomics), a one-block LDS scan, and a scatter
-//      whose ranks come from wave ballots plus per-wave counts, so equal keys
-//      keep position order;
-//   3. tile-segmented reduction over the sorted positions: each block owns
-//      ST positions and sums every run of equal keys in position order in
-//      f32 -- the reference's own order, so a run inside one tile gives a
-//      bit-identical row -- writing complete runs straight to the output and
-//      runs cut by a tile edge to per-tile partial slots;
-//   4. fix-up: a key spanning several tiles adds its partial slots in tile
-//      order in float64 (16 waves split the slots, so a key that owns a third
-//      of all positions is not serialised on one wave);
-//   5. rows of absent keys are zero-filled.
-// Every block does the same amount of work whatever the id distribution.
+// VJP without float atomics (6 launches for 16-bit keys):
+//   1. stable LSD radix sort of (key, position) by 8-bit digits, a histogram
+//      and a scatter kernel per pass; keys are the ids wrapped to [0, len),
+//      out-of-range ids get the sentinel key `len` (never summed) and raise
+//      the guard flag; the first scatter flags every key that occurs;
+//   2. segmented reduction over the sorted positions: one wave per (tile of
+//      <= 64 positions, 64-vector column chunk) sums every run of equal keys
+//      in position order in f32 -- the reference's own order, so a run of at
+//      most one tile's length gives a bit-identical row -- writing it straight
+//      to the output; a longer run leaves per-tile partial sums; the same
+//      launch writes the zero rows of keys that never occur;
+//   3. fix-up: each key of a longer run adds its partial sums in tile order in
+//      float64.
+// Every wave of step 2 does the same amount of work whatever the id
+// distribution (a key owning a third of all positions is spread over many
+// tiles).
 #include <algorithm>
 #include <type_traits>
 
@@ -67,7 +66,7 @@ __global__ __launch_bounds__(BS) void gather_k(const float* __restrict__ src, in
       if (!ok && threadIdx.x == 0) atomicOr(guard, 1);
     }
   }
-  for (int64_t c = threadIdx.x; c < units; c += BS) {
+  for (int64_t c = threadIdx.x; c < units; c += blockDim.x) {
     if constexpr (VEC) {
       f4 v[GRPB];
 #pragma unroll
@@ -104,121 +103,162 @@ __global__ __launch_bounds__(BS) void gather_elem_k(const float* __restrict__ sr
 }
 
 // ---------------------------------------------------------------------------
-// VJP step 1: keys. Out-of-range ids become the sentinel key `len` (never
-// summed) and raise the guard flag.
+// VJP, sort: stable LSD radix sort of (key, position) pairs, 8-bit digits.
+// Keys are the ids wrapped to [0, len); an out-of-range id gets the sentinel
+// key `len` (sorted last, never summed) and raises the guard flag. A block owns
+// a tile of SBS * IPT consecutive elements. Per pass:
+//   sort_hist_k    per-tile digit counts (LDS integer atomics: exact) into a
+//                  tile-major table cnt[tile * 256 + digit];
+//   sort_scatter_k each block first derives its tile's 256 output offsets
+//                  from the whole table (digit-major exclusive prefix: the
+//                  stable order), then sends each element to its digit's
+//                  offset plus the number of earlier elements of the tile with
+//                  that digit (wave ballots + per-wave LDS counts).
+// Tables of more than 256 tiles are scanned once by sort_offsets_k instead.
+// The first pass reads the int64 ids directly and flags every key present.
 
-__global__ __launch_bounds__(BS) void keys_k(const int64_t* __restrict__ idx, int64_t n, int64_t len,
-                                             int* __restrict__ keys, int* __restrict__ pos, int* __restrict__ guard) {
-  for (int64_t p = (int64_t)blockIdx.x * BS + threadIdx.x; p < n; p += (int64_t)gridDim.x * BS) {
-    bool ok;
-    const int64_t id = wrap_id(idx[p], len, ok);
-    if (!ok) atomicOr(guard, 1);
-    keys[p] = ok ? (int)id : (int)len;
-    pos[p] = (int)p;
+constexpr int SBS = 256;
+constexpr int SCAN_REG = 64;     // table rows one thread holds at a time
+constexpr int SELF_SCAN_MAX = 256;  // tiles up to which each scatter block scans the table itself
+constexpr int SEEN = 1024;       // LDS filter of recently flagged keys
+
+__device__ __forceinline__ int key_of(const int64_t* __restrict__ idx, int64_t p, int64_t len, int* guard) {
+  bool ok;
+  const int64_t id = wrap_id(idx[p], len, ok);
+  if (!ok) atomicOr(guard, 1);
+  return ok ? (int)id : (int)len;
+}
+
+// Exclusive scan of the 256 per-digit values `v` of the block (thread t
+// holds digit t's value); returns thread t's exclusive prefix. `ws` holds 4 ints.
+__device__ __forceinline__ int block_excl_scan256(int v, int* ws) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) ws[w] = inc;
+  __syncthreads();
+  int pre = 0;
+#pragma unroll
+  for (int q = 0; q < SBS / 64; ++q) pre += (q < w) ? ws[q] : 0;
+  return pre + inc - v;
+}
+
+// Digit t's counts (thread t) summed over all `ntiles` tiles of the table,
+// and over the tiles before `upto`.
+__device__ __forceinline__ void column_sums(const int* __restrict__ tab, int ntiles, int upto, int& total,
+                                            int& before) {
+  total = 0;
+  before = 0;
+  for (int jb = 0; jb < ntiles; jb += SCAN_REG) {
+    int v[SCAN_REG];
+#pragma unroll
+    for (int q = 0; q < SCAN_REG; ++q) {
+      const int j = min(jb + q, ntiles - 1);  // always in range: loads issue together
+      v[q] = tab[(int64_t)j * 256 + threadIdx.x];
+    }
+#pragma unroll
+    for (int q = 0; q < SCAN_REG; ++q) {
+      total += (jb + q < ntiles) ? v[q] : 0;
+      before += (jb + q < upto) ? v[q] : 0;
+    }
   }
 }
 
-// ---------------------------------------------------------------------------
-// VJP step 2: stable LSD radix sort of (key, position), 8-bit digits.
-// A block owns a tile of RT consecutive elements (256 threads x 8 items).
-
-constexpr int RT = 2048;
-
-// hist[d * ntiles + tile] = number of elements of `tile` whose digit is d.
-__global__ __launch_bounds__(BS) void radix_hist_k(const int* __restrict__ keys, int64_t n, int shift, int ntiles,
-                                                   int* __restrict__ hist) {
+template <int IPT, bool FROM_IDX>
+__global__ __launch_bounds__(SBS) void sort_hist_k(const int64_t* __restrict__ idx, const int* __restrict__ keys,
+                                                   int64_t n, int64_t len, int shift, int* __restrict__ tab,
+                                                   int* __restrict__ present, int* __restrict__ owner_count,
+                                                   int* guard) {
   __shared__ int cnt[256];
   const int t = threadIdx.x;
   cnt[t] = 0;
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * RT;
+  const int64_t base = (int64_t)blockIdx.x * (SBS * IPT);
+  int k[IPT];
 #pragma unroll
-  for (int i = 0; i < RT / BS; ++i) {
-    const int64_t p = base + i * BS + t;
-    if (p < n) atomicAdd(&cnt[(keys[p] >> shift) & 255], 1);  // LDS integer atomics: exact counts
+  for (int i = 0; i < IPT; ++i) {
+    const int64_t p = base + i * SBS + t;
+    k[i] = -1;
+    if (p < n) k[i] = FROM_IDX ? key_of(idx, p, len, guard) : keys[p];
   }
+#pragma unroll
+  for (int i = 0; i < IPT; ++i)
+    if (k[i] >= 0) atomicAdd(&cnt[(k[i] >> shift) & 255], 1);  // LDS integer atomics: exact counts
+  if (present)  // first pass: clear this call's present-key flags and owner count
+    for (int64_t v = (int64_t)blockIdx.x * SBS + t; v < len; v += (int64_t)gridDim.x * SBS) present[v] = 0;
+  if (owner_count && blockIdx.x == 0 && t == 0) *owner_count = 0;
   __syncthreads();
-  hist[(int64_t)t * ntiles + blockIdx.x] = cnt[t];
+  tab[(int64_t)blockIdx.x * 256 + t] = cnt[t];
 }
 
-// In-place exclusive scan of m ints by one block of 1024 threads, in LDS
-// chunks of 8192 (coalesced loads/stores; padded LDS rows avoid bank conflicts).
-constexpr int SCAN_T = 1024;
-constexpr int SCAN_CHUNK = 8 * SCAN_T;
+// One block: the count table becomes the offset table, in place.
+__global__ __launch_bounds__(SBS) void sort_offsets_k(int* tab, int ntiles) {
+  __shared__ int ws[SBS / 64];
+  const int t = threadIdx.x;
+  int total, unused;
+  column_sums(tab, ntiles, 0, total, unused);
+  int run = block_excl_scan256(total, ws);
+  for (int j = 0; j < ntiles; ++j) {
+    const int x = tab[(int64_t)j * 256 + t];
+    tab[(int64_t)j * 256 + t] = run;
+    run += x;
+  }
+}
 
-__device__ __forceinline__ int pad_idx(int e) { return e + (e >> 3); }
-
-__global__ __launch_bounds__(SCAN_T) void scan_k(int* a, int64_t m) {
-  __shared__ int buf[SCAN_CHUNK + SCAN_CHUNK / 8];
-  __shared__ int wsum[SCAN_T / 64];
-  __shared__ int carry_s;
+template <int IPT, bool FROM_IDX, bool SELF_SCAN>
+__global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict__ idx, const int* __restrict__ keys,
+                                                      const int* __restrict__ vals, int64_t n, int64_t len, int shift,
+                                                      int ntiles, const int* __restrict__ tab,
+                                                      int* __restrict__ keys_out, int* __restrict__ vals_out,
+                                                      int* __restrict__ present, int* guard) {
+  __shared__ int base[256];
+  __shared__ int cnt[SBS / 64][256];
+  __shared__ int ws[SBS / 64];
+  __shared__ int seen[SEEN];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  if (t == 0) carry_s = 0;
-  for (int64_t base = 0; base < m; base += SCAN_CHUNK) {
+  const int64_t tile0 = (int64_t)blockIdx.x * (SBS * IPT);
+  // all of this thread's elements up front: one load latency for the tile
+  int kk[IPT], vv[IPT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = i * SCAN_T + t;
-      buf[pad_idx(e)] = (base + e < m) ? a[base + e] : 0;
+  for (int r = 0; r < IPT; ++r) {
+    const int64_t p = tile0 + r * SBS + t;
+    kk[r] = 0;
+    vv[r] = 0;
+    if (p < n) {
+      kk[r] = FROM_IDX ? key_of(idx, p, len, guard) : keys[p];
+      vv[r] = FROM_IDX ? (int)p : vals[p];
     }
+  }
+  if constexpr (SELF_SCAN) {
+    int total, before;
+    column_sums(tab, ntiles, (int)blockIdx.x, total, before);
+    base[t] = block_excl_scan256(total, ws) + before;
+  } else {
+    base[t] = tab[(int64_t)blockIdx.x * 256 + t];
+  }
+  if constexpr (FROM_IDX) {
+    // flag every key present; the LDS filter drops repeats of hot keys
+    for (int q = t; q < SEEN; q += SBS) seen[q] = -1;
     __syncthreads();
-    int v[8], sum = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      v[k] = buf[pad_idx(t * 8 + k)];
-      sum += v[k];
-    }
-    // inclusive wave scan of per-thread sums
-    int inc = sum;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(inc, d, 64);
-      if (lane >= d) inc += o;
-    }
-    if (lane == 63) wsum[w] = inc;
-    __syncthreads();
-    if (t == 0) {
-      int run = 0;
-      for (int q = 0; q < SCAN_T / 64; ++q) {
-        const int x = wsum[q];
-        wsum[q] = run;
-        run += x;
+    for (int r = 0; r < IPT; ++r) {
+      const int k = kk[r];
+      if (tile0 + r * SBS + t < n && (uint64_t)k < (uint64_t)len && seen[k & (SEEN - 1)] != k) {
+        seen[k & (SEEN - 1)] = k;  // racing writers store the same flag: harmless
+        present[k] = 1;
       }
     }
-    __syncthreads();
-    int run = carry_s + wsum[w] + inc - sum;  // exclusive prefix of this thread
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      buf[pad_idx(t * 8 + k)] = run;
-      run += v[k];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int e = i * SCAN_T + t;
-      if (base + e < m) a[base + e] = buf[pad_idx(e)];
-    }
-    if (t == SCAN_T - 1) carry_s = run;
-    __syncthreads();
   }
-}
-
-// Stable scatter: element r*256 + t of a tile goes after every earlier element
-// with the same digit. Ranks within a wave come from ballots; counts of the
-// earlier waves of the same round from LDS.
-__global__ __launch_bounds__(BS) void radix_scatter_k(const int* __restrict__ keys, const int* __restrict__ vals,
-                                                      int64_t n, int shift, int ntiles, const int* __restrict__ offs,
-                                                      int* __restrict__ keys_out, int* __restrict__ vals_out) {
-  __shared__ int base[256];
-  __shared__ int cnt[BS / 64][256];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  base[t] = offs[(int64_t)t * ntiles + blockIdx.x];
   const unsigned long long lt = (1ull << lane) - 1ull;
-  const int64_t tile0 = (int64_t)blockIdx.x * RT;
-  for (int r = 0; r < RT / BS; ++r) {
-    const int64_t p = tile0 + r * BS + t;
+#pragma unroll
+  for (int r = 0; r < IPT; ++r) {
+    const int64_t p = tile0 + r * SBS + t;
     const bool valid = p < n;
-    const int k = valid ? keys[p] : 0;
-    const int v = valid ? vals[p] : 0;
+    const int k = kk[r], v = vv[r];
     const int d = (k >> shift) & 255;
     unsigned long long peers = __ballot(valid);
 #pragma unroll
@@ -228,7 +268,7 @@ __global__ __launch_bounds__(BS) void radix_scatter_k(const int* __restrict__ ke
       peers &= bit ? m : ~m;
     }
 #pragma unroll
-    for (int q = 0; q < BS / 64; ++q) cnt[q][t] = 0;
+    for (int q = 0; q < SBS / 64; ++q) cnt[q][t] = 0;
     __syncthreads();
     if (valid && (__ffsll((long long)peers) - 1) == lane) cnt[w][d] = __popcll(peers);
     __syncthreads();
@@ -236,169 +276,275 @@ __global__ __launch_bounds__(BS) void radix_scatter_k(const int* __restrict__ ke
       int pre = base[d];
       for (int q = 0; q < w; ++q) pre += cnt[q][d];
       const int dst = pre + __popcll(peers & lt);
-      keys_out[dst] = k;
-      vals_out[dst] = v;
+      if ((uint64_t)dst < (uint64_t)n) {
+        keys_out[dst] = k;
+        vals_out[dst] = v;
+      } else {
+        atomicOr(guard, 2);  // inconsistent offsets: reported, never written out of range
+      }
     }
     __syncthreads();
     int add = 0;
 #pragma unroll
-    for (int q = 0; q < BS / 64; ++q) add += cnt[q][t];
+    for (int q = 0; q < SBS / 64; ++q) add += cnt[q][t];
     base[t] += add;
     __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------------
-// VJP step 3: tile-segmented reduction. A block owns ST consecutive sorted
-// positions; every run of equal keys inside the tile is summed in position
-// order. A run that neither continues from the previous tile nor into the
-// next one is complete: its sum is the output row. Otherwise the sum goes to
-// a partial slot of the tile: slot 2*tile+1 for the run that continues into
-// the next tile, slot 2*tile for the first run continuing from the previous.
+// VJP, segmented reduction. The sorted positions are cut into tiles of `st`
+// (<= 64) positions; one wave owns a (tile, 64-column-vector chunk) pair and
+// holds the tile's keys and positions one per lane. Every run of equal keys is
+// summed in position order in f32 -- the reference's own order, so such a run
+// gives a bit-identical row:
+//  * a run inside the tile is written to its output row;
+//  * a run that starts in the tile and ends in the next one is finished by
+//    this wave, which reads on into the next tile's positions (the next tile's
+//    wave skips it);
+//  * a longer run (a "long key") is summed per tile into partial slots --
+//    2*tile+1 where it continues into the next tile, 2*tile where it ends --
+//    and the tile where it starts joins the owner list while the tile where it
+//    ends records itself in end_tile[key]; seg_fixup_k adds the slots.
+// Blocks past the segment work write zero rows for keys that never occur
+// (ZR rows per block), so those writes overlap the gathers.
 
-constexpr int ST = 128;
-constexpr int SU = 8;  // rows in flight per thread
+constexpr int SEG_U = 8;  // rows in flight per lane
+constexpr int ZR = 4;
 
 template <bool VEC>
-__global__ __launch_bounds__(BS) void seg_tile_k(const float* __restrict__ g, int64_t outer, int64_t n, int64_t inner,
-                                                 int64_t len, const int* __restrict__ skeys,
-                                                 const int* __restrict__ perm, float* __restrict__ grad,
-                                                 float* __restrict__ part, int* __restrict__ present) {
-  __shared__ int key_s[ST + 2];  // [0] = key before the tile (-1 if none), [cnt+1] = key after
-  __shared__ int pos_s[ST];
-  const int t = threadIdx.x;
-  const int64_t p0 = (int64_t)blockIdx.x * ST;
-  const int cnt = (int)min<int64_t>(ST, n - p0);
-  if (t < cnt) {
-    key_s[t + 1] = skeys[p0 + t];
-    pos_s[t] = perm[p0 + t];
-  }
-  if (t == 0) key_s[0] = p0 > 0 ? skeys[p0 - 1] : -1;
-  if (t == 1) key_s[cnt + 1] = p0 + cnt < n ? skeys[p0 + cnt] : -1;
-  __syncthreads();
-  if (t == 0) {  // mark present keys (plain stores of 1: order-free)
-    for (int i = 0; i < cnt; ++i)
-      if (key_s[i + 1] != key_s[i] && key_s[i + 1] < len) present[key_s[i + 1]] = 1;
-  }
+__global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, int64_t outer, int64_t n,
+                                                  int64_t inner, int64_t len, const int* __restrict__ skeys,
+                                                  const int* __restrict__ perm, float* __restrict__ grad,
+                                                  float* __restrict__ part, const int* __restrict__ present,
+                                                  int* __restrict__ owners, int* __restrict__ owner_count,
+                                                  int* __restrict__ end_tile, int st, int64_t stiles, int chunks,
+                                                  int64_t seg_blocks) {
+  using V = typename std::conditional<VEC, f4, float>::type;
   const int64_t units = VEC ? inner / 4 : inner;
-  const int64_t slot_head = 2 * (int64_t)blockIdx.x, slot_tail = slot_head + 1;
+  if ((int64_t)blockIdx.x >= seg_blocks) {
+    const int64_t v0 = ((int64_t)blockIdx.x - seg_blocks) * ZR;
+    for (int r = 0; r < ZR; ++r) {
+      const int64_t v = v0 + r;
+      if (v >= len || present[v]) continue;
+      for (int64_t o = 0; o < outer; ++o) {
+        float* dst = grad + (o * len + v) * inner;
+        for (int64_t c = threadIdx.x; c < units; c += 256) {
+          if constexpr (VEC) __builtin_nontemporal_store(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + c);
+          else __builtin_nontemporal_store(0.f, dst + c);
+        }
+      }
+    }
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = item / chunks;
+  const int chunk = (int)(item - tile * chunks);
+  if (tile >= stiles) return;  // uniform per wave
+  const int64_t p0 = tile * st;
+  const int cnt = (int)min<int64_t>(st, n - p0);
+  const int64_t p1 = p0 + cnt;                       // first position of the next tile
+  const int cnt2 = (int)min<int64_t>(st, n - p1);    // its size (<= 0 if none)
+  // this tile and, speculatively, the next one (for a run reaching into it)
+  const int my_key = lane < cnt ? skeys[p0 + lane] : -2;
+  const int my_pos = lane < cnt ? perm[p0 + lane] : 0;
+  const int nx_key = lane < cnt2 ? skeys[p1 + lane] : -2;
+  const int nx_pos = lane < cnt2 ? perm[p1 + lane] : 0;
+  const int key_before = p0 > 0 ? skeys[p0 - 1] : -1;
+  const int key_after2 = p1 + cnt2 < n ? skeys[p1 + max(cnt2, 0)] : -1;  // first key after the next tile
+  const int key_prev2 = p0 - st - 1 >= 0 ? skeys[p0 - st - 1] : -1;      // key before the previous tile
+  const int key_after = __builtin_amdgcn_readfirstlane(nx_key) ;          // -2 when there is no next tile
+  const int nxt0 = __shfl_down(my_key, 1, 64);
+  const int nxt = (lane == cnt - 1) ? key_after : nxt0;
+  // run ends inside the tile: key changes, or the tile's last position
+  const unsigned long long ends = __ballot(lane < cnt && (nxt != my_key || lane == cnt - 1));
+  const int key0 = __builtin_amdgcn_readfirstlane(my_key);
+  const int keyl = __builtin_amdgcn_readlane(my_key, cnt - 1);
+  const bool head_inc = key_before == key0;   // first run continues from the previous tile
+  const bool tail_inc = key_after == keyl;    // last run continues into the next tile
+  const bool single = key0 == keyl;           // the tile holds one key
+  // tail run that starts here and continues: ends in the next tile (extend)
+  // or runs past it (long key, this tile owns it)
+  const bool tail_here = tail_inc && !(head_inc && single);
+  const unsigned long long nx_diff = __ballot(lane < cnt2 && nx_key != keyl);
+  const bool tail_long = tail_here && nx_diff == 0 && key_after2 == keyl;
+  const bool tail_ext = tail_here && !tail_long;
+  const int ext_len = tail_ext ? (nx_diff ? (__ffsll((long long)nx_diff) - 1) : cnt2) : 0;
+  // head run that continues from the previous tile and ends here: skipped if
+  // it started in the previous tile (that wave finished it), else a long key
+  const bool head_end = head_inc && !(tail_inc && single);
+  const bool head_skip = head_end && key_prev2 != key0;
+  if (chunk == 0 && lane == 0) {
+    if (tail_long && (uint64_t)keyl < (uint64_t)len) owners[atomicAdd(owner_count, 1)] = (int)tile;
+    if (head_end && !head_skip && (uint64_t)key0 < (uint64_t)len) end_tile[key0] = (int)tile;
+  }
+  const int first = head_skip ? __ffsll((long long)ends) : 0;  // one past the head run's end
+  const int64_t u = (int64_t)chunk * 64 + lane;
+  const bool active = u < units;
+  const int64_t slot_head = 2 * tile, slot_tail = slot_head + 1;
   for (int64_t o = 0; o < outer; ++o) {
     const float* gb = g + o * n * inner;
-    for (int64_t u = t; u < units; u += BS) {
-      using V = typename std::conditional<VEC, f4, float>::type;
-      V acc = V{};
-      int start = 0;
-      for (int i = 0; i < cnt; i += SU) {
-        V vals[SU];
+    V acc = V{};
+    int start = first;
+    for (int i = first; i < cnt; i += SEG_U) {
+      V vals[SEG_U];
 #pragma unroll
-        for (int j = 0; j < SU; ++j) {
-          if (i + j < cnt) {
-            const float* row = gb + (int64_t)pos_s[i + j] * inner;
+      for (int j = 0; j < SEG_U; ++j) {
+        vals[j] = V{};
+        const int pj = __builtin_amdgcn_readlane(my_pos, (i + j) & 63);  // uniform; used only if i + j < cnt
+        if (i + j < cnt && active && (uint64_t)pj < (uint64_t)n) {
+          const float* row = gb + (int64_t)pj * inner;
+          if constexpr (VEC) vals[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(row) + u);
+          else vals[j] = __builtin_nontemporal_load(row + u);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < SEG_U; ++j) {
+        const int q = i + j;
+        if (q >= cnt) break;
+        acc = acc + vals[j];
+        if (((ends >> q) & 1ull) && !(tail_ext && q == cnt - 1)) {  // run [start, q] ends here
+          const int key = __builtin_amdgcn_readlane(my_key, q);
+          if ((uint64_t)key < (uint64_t)len && active) {
+            const bool to_tail = tail_inc && q == cnt - 1;
+            const bool to_head = !to_tail && head_inc && start == 0;
+            float* dst;
+            if (to_tail) dst = part + (slot_tail * outer + o) * inner;
+            else if (to_head) dst = part + (slot_head * outer + o) * inner;
+            else dst = grad + (o * len + key) * inner;
+            if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
+            else dst[u] = acc;
+          }
+          acc = V{};
+          start = q + 1;
+        }
+      }
+    }
+    if (tail_ext) {  // the last run goes on into the next tile's first ext_len positions
+      for (int i = 0; i < ext_len; i += SEG_U) {
+        V vals[SEG_U];
+#pragma unroll
+        for (int j = 0; j < SEG_U; ++j) {
+          vals[j] = V{};
+          const int pj = __builtin_amdgcn_readlane(nx_pos, (i + j) & 63);
+          if (i + j < ext_len && active && (uint64_t)pj < (uint64_t)n) {
+            const float* row = gb + (int64_t)pj * inner;
             if constexpr (VEC) vals[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(row) + u);
-            else vals[j] = row[u];
+            else vals[j] = __builtin_nontemporal_load(row + u);
           }
         }
 #pragma unroll
-        for (int j = 0; j < SU; ++j) {
-          const int q = i + j;
-          if (q >= cnt) break;
-          acc = acc + vals[j];
-          const int key = key_s[q + 1];
-          if (key_s[q + 2] != key || q == cnt - 1) {  // run [start, q] ends here
-            if (key < len) {
-              const bool head_inc = (start == 0) && (key_s[0] == key);
-              const bool tail_inc = (q == cnt - 1) && (key_s[cnt + 1] == key);
-              float* dst;
-              if (!head_inc && !tail_inc) dst = grad + (o * len + key) * inner;
-              else dst = part + ((tail_inc ? slot_tail : slot_head) * outer + o) * inner;
-              if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
-              else dst[u] = acc;
-            }
-            acc = V{};
-            start = q + 1;
-          }
-        }
+        for (int j = 0; j < SEG_U; ++j)
+          if (i + j < ext_len) acc = acc + vals[j];
+      }
+      if ((uint64_t)keyl < (uint64_t)len && active) {
+        float* dst = grad + (o * len + keyl) * inner;
+        if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
+        else dst[u] = acc;
       }
     }
   }
 }
 
-// VJP step 4: a segment spanning tiles ta..tb is owned by ta; its partials
-// are the tail slots of ta..tb-1 and the head slot of tb, added in tile order
-// in float64. Block: 16 waves x 64 lanes, blockIdx.y = column chunk.
-constexpr int FX_W = 16;
+// ---------------------------------------------------------------------------
+// VJP, fix-up of long keys. Work unit = (owner, 16-vector column chunk);
+// blocks walk the units grid-stride, bounded by the owner count. In a unit,
+// thread (s, c) adds column c of slots s, s+16, s+32, ... in order in float64
+// (FXU slots in flight); the 16 slot sums are then combined in a fixed tree
+// (wave shuffles over the 4 slot lanes a wave holds, then the 4 waves in
+// order). Slots: tail slots of tiles ta..tb-1, head slot of tb.
+
+constexpr int FXU = 16;
 
 template <bool VEC>
-__global__ __launch_bounds__(64 * FX_W) void seg_fixup_k(int64_t outer, int64_t n, int64_t inner, int64_t len,
-                                                         const int* __restrict__ skeys,
-                                                         const float* __restrict__ part, float* __restrict__ grad) {
-  const int64_t tile = blockIdx.x;
-  const int64_t p0 = tile * ST;
-  const int64_t p1 = min<int64_t>(p0 + ST, n);
-  if (p1 >= n) return;  // nothing continues past the last tile
-  const int klast = skeys[p1 - 1];
-  if (skeys[p1] != klast || klast >= len) return;                       // tail run ends in this tile
-  if (p0 > 0 && skeys[p0] == klast && skeys[p0 - 1] == klast) return;  // run started in an earlier tile
-  // last position of the segment: upper_bound over [p1, n) - 1
-  int64_t lo = p1, hi = n;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (skeys[mid] <= klast) lo = mid + 1;
-    else hi = mid;
-  }
-  const int64_t tb = (lo - 1) / ST;
-  const int64_t m = tb - tile + 1;  // partial slots
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t u = (int64_t)blockIdx.y * 64 + lane;
+__global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t n, int64_t inner, int64_t len, int st,
+                                                   int64_t stiles, const int* __restrict__ skeys,
+                                                   const int* __restrict__ owners, const int* __restrict__ owner_count,
+                                                   const int* __restrict__ end_tile, const float* __restrict__ part,
+                                                   float* __restrict__ grad, int c16, int* guard) {
+  using V = typename std::conditional<VEC, f4, float>::type;
+  constexpr int NC = VEC ? 4 : 1;
+  __shared__ double red[4][16][NC];
   const int64_t units = VEC ? inner / 4 : inner;
-  __shared__ double red[FX_W][64][VEC ? 4 : 1];
-  for (int64_t o = 0; o < outer; ++o) {
-    double a[4] = {0.0, 0.0, 0.0, 0.0};
-    if (u < units) {
-      for (int64_t j = wv; j < m; j += FX_W) {
-        const int64_t slot = (j < m - 1) ? 2 * (tile + j) + 1 : 2 * tb;
-        const float* src = part + (slot * outer + o) * inner;
-        if constexpr (VEC) {
-          const f4 v = reinterpret_cast<const f4*>(src)[u];
-          a[0] += v.x; a[1] += v.y; a[2] += v.z; a[3] += v.w;
-        } else {
-          a[0] += src[u];
-        }
-      }
+  const int sl = threadIdx.x >> 4, c = threadIdx.x & 15, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t nunits = (int64_t)(*owner_count) * c16;
+  for (int64_t wk = blockIdx.x; wk < nunits; wk += gridDim.x) {
+    const int64_t oi = wk / c16;
+    const int chunk = (int)(wk - oi * c16);
+    const int64_t ta = owners[oi];
+    const int64_t p1 = min<int64_t>(ta * st + st, n);
+    const int key = skeys[p1 - 1];
+    const int64_t tb = ((uint64_t)key < (uint64_t)len) ? end_tile[key] : -1;
+    if (tb <= ta + 1 || tb >= stiles) {  // inconsistent: reported, nothing written
+      if (threadIdx.x == 0) atomicOr(guard, 2);
+      continue;
     }
-#pragma unroll
-    for (int c = 0; c < (VEC ? 4 : 1); ++c) red[wv][lane][c] = a[c];
-    __syncthreads();
-    if (wv == 0 && u < units) {
-      double r[4] = {0.0, 0.0, 0.0, 0.0};
-      for (int q = 0; q < FX_W; ++q)
-#pragma unroll
-        for (int c = 0; c < (VEC ? 4 : 1); ++c) r[c] += red[q][lane][c];
-      float* dst = grad + (o * len + klast) * inner;
-      if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = f4{(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
-      else dst[u] = (float)r[0];
-    }
-    __syncthreads();
-  }
-}
-
-// VJP step 5: rows of keys that never occur are zero.
-constexpr int ZR = 4;  // rows per block
-
-template <bool VEC>
-__global__ __launch_bounds__(BS) void zero_absent_k(int64_t outer, int64_t len, int64_t inner,
-                                                    const int* __restrict__ present, float* __restrict__ grad) {
-  const int64_t units = VEC ? inner / 4 : inner;
-  for (int r = 0; r < ZR; ++r) {
-    const int64_t v = (int64_t)blockIdx.x * ZR + r;
-    if (v >= len || present[v]) continue;
+    const int64_t m = tb - ta + 1;  // partial slots
+    const int64_t u = (int64_t)chunk * 16 + c;
+    const bool active = u < units;
     for (int64_t o = 0; o < outer; ++o) {
-      float* dst = grad + (o * len + v) * inner;
-      for (int64_t u = threadIdx.x; u < units; u += BS) {
-        if constexpr (VEC) __builtin_nontemporal_store(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + u);
-        else dst[u] = 0.f;
+      double a[NC];
+#pragma unroll
+      for (int q = 0; q < NC; ++q) a[q] = 0.0;
+      for (int64_t j0 = sl; j0 < m; j0 += 16 * FXU) {
+        V v[FXU];
+#pragma unroll
+        for (int q = 0; q < FXU; ++q) {
+          const int64_t j = min<int64_t>(j0 + 16 * q, m - 1);  // in range: loads issue together
+          const int64_t slot = (j < m - 1) ? 2 * (ta + j) + 1 : 2 * tb;
+          v[q] = active ? reinterpret_cast<const V*>(part + (slot * outer + o) * inner)[u] : V{};
+        }
+#pragma unroll
+        for (int q = 0; q < FXU; ++q) {
+          if (j0 + 16 * q < m) {
+            if constexpr (VEC) {
+              a[0] += v[q].x; a[1] += v[q].y; a[2] += v[q].z; a[3] += v[q].w;
+            } else {
+              a[0] += v[q];
+            }
+          }
+        }
       }
+      // lanes c, c+16, c+32, c+48 of a wave hold 4 slot lanes of column c
+#pragma unroll
+      for (int q = 0; q < NC; ++q) {
+        a[q] += __shfl_xor(a[q], 16, 64);
+        a[q] += __shfl_xor(a[q], 32, 64);
+      }
+      if (lane < 16)
+#pragma unroll
+        for (int q = 0; q < NC; ++q) red[w][c][q] = a[q];
+      __syncthreads();
+      if (threadIdx.x < 16 && active) {
+        double r[NC];
+#pragma unroll
+        for (int q = 0; q < NC; ++q) r[q] = (red[0][c][q] + red[1][c][q]) + (red[2][c][q] + red[3][c][q]);
+        float* dst = grad + (o * len + key) * inner;
+        if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = f4{(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
+        else dst[u] = (float)r[0];
+      }
+      __syncthreads();
     }
+  }
+}
+
+template <int IPT>
+void sort_pass(hipStream_t s, int ps, int passes, int64_t n, int64_t len, int ntiles, const int64_t* idx,
+               const int* ka, const int* va, int* kb, int* vb, int* tab, int* present, int* owner_count) {
+  (void)passes;
+  const int shift = 8 * ps;
+  const unsigned nb = (unsigned)ntiles;
+  const bool self = ntiles <= SELF_SCAN_MAX;
+  if (ps == 0) sort_hist_k<IPT, true><<<nb, SBS, 0, s>>>(idx, nullptr, n, len, shift, tab, present, owner_count, guard_flag());
+  else sort_hist_k<IPT, false><<<nb, SBS, 0, s>>>(nullptr, ka, n, len, shift, tab, nullptr, nullptr, guard_flag());
+  if (!self) sort_offsets_k<<<1, SBS, 0, s>>>(tab, ntiles);
+  if (ps == 0) {
+    if (self) sort_scatter_k<IPT, true, true><<<nb, SBS, 0, s>>>(idx, nullptr, nullptr, n, len, shift, ntiles, tab, kb, vb, present, guard_flag());
+    else sort_scatter_k<IPT, true, false><<<nb, SBS, 0, s>>>(idx, nullptr, nullptr, n, len, shift, ntiles, tab, kb, vb, present, guard_flag());
+  } else {
+    if (self) sort_scatter_k<IPT, false, true><<<nb, SBS, 0, s>>>(nullptr, ka, va, n, len, shift, ntiles, tab, kb, vb, nullptr, guard_flag());
+    else sort_scatter_k<IPT, false, false><<<nb, SBS, 0, s>>>(nullptr, ka, va, n, len, shift, ntiles, tab, kb, vb, nullptr, guard_flag());
   }
 }
 
@@ -431,8 +577,12 @@ int oxi_index_select(const float* src, int64_t outer, int64_t len, int64_t inner
     const bool vec = inner % 4 == 0 && al16(src) && al16(out);
     const int64_t blocks = ceil_div(rows, GRPB);
     if (blocks >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select: too many rows");
-    if (vec) gather_k<true><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
-    else gather_k<false><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
+    // threads per block: the row's vector count rounded up to whole waves
+    // (192 for a 768-float row), at most BS
+    const int64_t units = vec ? inner / 4 : inner;
+    const unsigned bt = (unsigned)std::min<int64_t>(BS, ceil_div(units, 64) * 64);
+    if (vec) gather_k<true><<<dim3((unsigned)blocks), dim3(bt), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
+    else gather_k<false><<<dim3((unsigned)blocks), dim3(bt), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
   } else {
     const int64_t blocks = std::min<int64_t>(ceil_div(rows * inner, BS), (int64_t)cu_count() * 32);
     gather_elem_k<<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
@@ -449,16 +599,29 @@ int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inn
   OXI_CHECK_INIT();
   if (n == 0) return oxi_fill(grad, total_out, 0.f);
   if (!g || !idx) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: NULL tensor pointer");
+  if (len + 1 >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: dim too large");
   hipStream_t s = stream();
-  const int64_t rtiles = ceil_div(n, RT);
-  const int64_t stiles = ceil_div(n, ST);
-  if (rtiles * 256 > ((int64_t)1 << 31) || len + 1 >= ((int64_t)1 << 31))
-    return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many indices");
+  // sort tiles: 2, 8 or 32 elements per thread, so that tables stay within
+  // SELF_SCAN_MAX tiles up to 2M indices
+  const int ipt = n <= 65536 ? 2 : (n <= 524288 ? 8 : 32);
+  const int64_t rtiles = ceil_div(n, (int64_t)SBS * ipt);
+  if (rtiles * 256 >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many indices");
   int passes = 0;
   for (int64_t m = len; m > 0; m >>= 8) ++passes;  // keys are in [0, len]
   if (passes == 0) passes = 1;
-  // workspace (ints): keys, pos, keys2, pos2 (n each), hist (256 * rtiles), present (len)
-  const size_t ints = 4 * (size_t)n + 256 * (size_t)rtiles + (size_t)len;
+  // segment tiles: as long as possible (fewer cut runs) while still giving
+  // every CU several waves
+  const bool vec = inner % 4 == 0 && al16(g) && al16(grad);
+  const int64_t units = vec ? inner / 4 : inner;
+  const int64_t chunks = ceil_div(units, 64);
+  const int64_t c16 = ceil_div(units, 16);
+  if (c16 >= (1 << 24)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: rows too wide");
+  int st = 64;
+  while (st > 16 && ceil_div(n, st) * chunks < 8 * (int64_t)cu_count()) st >>= 1;
+  const int64_t stiles = ceil_div(n, st);
+  // workspace (ints): keys, pos, keys2, pos2 (n each), count table
+  // (256 * rtiles), present (len), end_tile (len), owners (stiles), owner count
+  const size_t ints = 4 * (size_t)n + 256 * (size_t)rtiles + 2 * (size_t)len + (size_t)stiles + 1;
   Workspace wsi(ints * sizeof(int));
   Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(float));
   if (!wsi.p || !wsp.p) return OXI_OTHER;
@@ -466,37 +629,45 @@ int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inn
   int* pos = keys + n;
   int* keys2 = pos + n;
   int* pos2 = keys2 + n;
-  int* hist = pos2 + n;
-  int* present = hist + 256 * rtiles;
-  if (int rc = oxi_fill(reinterpret_cast<float*>(present), len, 0.f)) return rc;  // +0.0f is all-zero bits
-  const unsigned gb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, BS), (int64_t)cu_count() * 8));
-  keys_k<<<gb, BS, 0, s>>>(idx, n, len, keys, pos, guard_flag());
-  if (int rc = check_launch("index_select_bwd/keys")) return rc;
-  int *ka = keys, *va = pos, *kb = keys2, *vb = pos2;
+  int* tab = pos2 + n;
+  int* present = tab + 256 * rtiles;
+  int* end_tile = present + len;
+  int* owners = end_tile + len;
+  int* owner_count = owners + stiles;
+  // pass p reads (ka, va) and writes (kb, vb); pass 0 reads the ids
+  const int* ka = nullptr;
+  const int* va = nullptr;
+  int* bufk[2] = {keys, keys2};
+  int* bufv[2] = {pos, pos2};
   for (int ps = 0; ps < passes; ++ps) {
-    const int shift = 8 * ps;
-    radix_hist_k<<<(unsigned)rtiles, BS, 0, s>>>(ka, n, shift, (int)rtiles, hist);
-    scan_k<<<1, SCAN_T, 0, s>>>(hist, 256 * rtiles);
-    radix_scatter_k<<<(unsigned)rtiles, BS, 0, s>>>(ka, va, n, shift, (int)rtiles, hist, kb, vb);
-    std::swap(ka, kb);
-    std::swap(va, vb);
+    int* kb = bufk[ps & 1];
+    int* vb = bufv[ps & 1];
+    if (ipt == 2) sort_pass<2>(s, ps, passes, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
+    else if (ipt == 8) sort_pass<8>(s, ps, passes, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
+    else sort_pass<32>(s, ps, passes, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
+    ka = kb;
+    va = vb;
   }
   if (int rc = check_launch("index_select_bwd/sort")) return rc;
-  const bool vec = inner % 4 == 0 && al16(g) && al16(grad);
   float* part = wsp.as<float>();
-  if (vec) seg_tile_k<true><<<(unsigned)stiles, BS, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present);
-  else seg_tile_k<false><<<(unsigned)stiles, BS, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present);
+  const int64_t seg_blocks = ceil_div(stiles * chunks, 4);
+  const int64_t blocks = seg_blocks + ceil_div(len, ZR);
+  if (blocks >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many rows");
+  if (vec)
+    seg_wave_k<true><<<(unsigned)blocks, 256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
+                                                      owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
+  else
+    seg_wave_k<false><<<(unsigned)blocks, 256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
+                                                       owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
   if (int rc = check_launch("index_select_bwd/segments")) return rc;
-  const int64_t units = vec ? inner / 4 : inner;
-  const dim3 fg((unsigned)stiles, (unsigned)ceil_div(units, 64));
-  if (fg.y > 65535) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: rows too wide");
-  if (vec) seg_fixup_k<true><<<fg, 64 * FX_W, 0, s>>>(outer, n, inner, len, ka, part, grad);
-  else seg_fixup_k<false><<<fg, 64 * FX_W, 0, s>>>(outer, n, inner, len, ka, part, grad);
-  if (int rc = check_launch("index_select_bwd/fixup")) return rc;
-  const unsigned gz = (unsigned)ceil_div(len, ZR);
-  if (vec) zero_absent_k<true><<<gz, BS, 0, s>>>(outer, len, inner, present, grad);
-  else zero_absent_k<false><<<gz, BS, 0, s>>>(outer, len, inner, present, grad);
-  return check_launch("index_select_bwd/zero");
+  const unsigned fb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(stiles * c16, 4 * (int64_t)cu_count()));
+  if (vec)
+    seg_fixup_k<true><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
+                                         grad, (int)c16, guard_flag());
+  else
+    seg_fixup_k<false><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
+                                          grad, (int)c16, guard_flag());
+  return check_launch("index_select_bwd/fixup");
 }
 
 int oxi_embedding_fwd(const float* W, const int64_t* ids, int64_t n, int64_t V, int64_t D, float* out) {

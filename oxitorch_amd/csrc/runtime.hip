@@ -29,6 +29,7 @@ struct Runtime {
   int cus = 0;
   hipStream_t stream = nullptr;
   int* guard = nullptr;  // device int, see guard_flag()
+  unsigned* done = nullptr;  // device counter, see done_counter()
   // caching allocator state
   std::multimap<size_t, void*> free_blocks;  // rounded size -> block
   std::unordered_map<void*, size_t> live;    // block -> rounded size
@@ -69,6 +70,9 @@ int init_locked(Runtime& r, int device) {
   if ((e = hipMalloc(&r.guard, sizeof(int))) != hipSuccess) return fail_hip(e, "hipMalloc(guard)");
   if ((e = hipMemsetAsync(r.guard, 0, sizeof(int), r.stream)) != hipSuccess)
     return fail_hip(e, "hipMemsetAsync(guard)");
+  if ((e = hipMalloc(&r.done, sizeof(unsigned))) != hipSuccess) return fail_hip(e, "hipMalloc(done counter)");
+  if ((e = hipMemsetAsync(r.done, 0, sizeof(unsigned), r.stream)) != hipSuccess)
+    return fail_hip(e, "hipMemsetAsync(done counter)");
   if ((e = hipStreamSynchronize(r.stream)) != hipSuccess) return fail_hip(e, "hipStreamSynchronize");
   r.device = device;
   return OXI_OK;
@@ -105,6 +109,7 @@ bool ensure_init() {
 
 hipStream_t stream() { return rt().stream; }
 int* guard_flag() { return rt().guard; }
+unsigned* done_counter() { return rt().done; }
 int cu_count() { return rt().cus > 0 ? rt().cus : 256; }
 
 void* ws_alloc(size_t bytes) {

@@ -117,10 +117,12 @@ def assert_sum_close(got, ref32, abs_sum, rtol=RTOL, atol=ATOL, what=""):
     assert not bad.any(), f"{what}: {bad.sum()} elements outside rtol*sum|terms|; max err {err.max():.3e}"
 
 
-def segmented_runs_in_one_tile(ids, V, tile=128):
-    """Keys whose stably-sorted run of positions lies inside one `tile`-position
-    block of the embedding VJP: their rows are summed in position order in f32
-    in one pass, exactly as the reference does, so they must match bitwise."""
+def segmented_runs_in_one_tile(ids, V, tile=16):
+    """Keys whose stably-sorted run of positions lies inside one aligned
+    `tile`-position block. The embedding VJP cuts the sorted positions into
+    aligned tiles of 16, 32 or 64, so such a run lies inside one of its tiles:
+    its row is summed in position order in f32 in one pass, exactly as the
+    reference does, and must match bitwise."""
     keys = np.where(np.asarray(ids) < 0, np.asarray(ids) + V, np.asarray(ids))
     counts = np.bincount(keys, minlength=V)
     start = np.concatenate([[0], np.cumsum(counts)[:-1]])

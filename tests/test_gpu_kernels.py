@@ -313,6 +313,59 @@ def test_index_select_general(hip, shape, dim, n):
     np.testing.assert_allclose(grad, ref.index_select_bwd(g, shape, dim, idx), rtol=1e-6, atol=1e-6)
 
 
+def _exact_bwd(g, shape, dim, idx):
+    """float64 scatter-add: the arbiter for long duplicate sums."""
+    L = shape[dim]
+    keys = np.where(idx < 0, idx + L, idx)
+    gm = np.moveaxis(g.astype(np.float64), dim, 0)
+    out = np.zeros((L,) + gm.shape[1:])
+    np.add.at(out, keys, gm)
+    return np.moveaxis(out, 0, dim)
+
+
+@pytest.mark.parametrize("case", ["skewed_outer", "one_key", "tile_runs", "two_hot_keys"])
+def test_index_select_bwd_run_shapes(hip, case):
+    """Runs shorter than, equal to and far longer than the VJP's position
+    tiles, on the scalar path (rows not a multiple of 4 floats) with several
+    outer slices, and on the vector path: values vs the oracle, long sums vs
+    float64, runs inside one aligned tile bit-exact, every call deterministic."""
+    from oracle import ref
+    say("index_select_bwd runs", case)
+    r = rng(21)
+    if case == "skewed_outer":   # outer 4, inner 130 (scalar), 6 keys over 500 positions
+        shape, dim = (4, 6, 130), 1
+        idx = np.minimum(r.zipf(1.3, 500) - 1, 5).astype(np.int64)
+    elif case == "one_key":      # a single key owning every position
+        shape, dim = (300, 64), 0
+        idx = np.full(5000, 17, np.int64)
+    elif case == "tile_runs":    # runs of 10..80 positions: cut by one or several tile edges
+        shape, dim = (400, 96), 0
+        idx = np.repeat(r.permutation(400)[:120], r.integers(10, 81, 120)).astype(np.int64)
+        r.shuffle(idx)
+    else:                        # two hot keys plus a uniform tail, negative ids included
+        shape, dim = (2000, 32), 0
+        idx = np.concatenate([np.full(3000, 5), np.full(2500, -1), r.integers(-2000, 2000, 4000)]).astype(np.int64)
+        r.shuffle(idx)
+    L = shape[dim]
+    out_shape = list(shape)
+    out_shape[dim] = idx.size
+    g = r.standard_normal(out_shape).astype(np.float32)
+    dg, di = D(hip, g), D(hip, idx)
+    got = hip.index_select_bwd(dg, shape, dim, di).numpy()
+    again = hip.index_select_bwd(dg, shape, dim, di).numpy()
+    hip.sync()
+    np.testing.assert_array_equal(got, again)
+    want32 = ref.index_select_bwd(g, shape, dim, idx)
+    exact = _exact_bwd(g, shape, dim, idx)
+    one = segmented_runs_in_one_tile(idx, L)
+    gm, wm = np.moveaxis(got, dim, 0), np.moveaxis(want32, dim, 0)
+    np.testing.assert_array_equal(gm[one], wm[one])
+    keys = np.where(idx < 0, idx + L, idx)
+    absent = np.bincount(keys, minlength=L) == 0
+    np.testing.assert_array_equal(gm[absent], 0.0)
+    assert_reduction_close(got, want32, exact, what=f"index_select_bwd {case}")
+
+
 def _zipf_ids(seed, shape, V):
     r = rng(seed)
     return np.minimum(r.zipf(1.1, shape) - 1, V - 1).astype(np.int64)
