@@ -44,9 +44,12 @@ __device__ __forceinline__ float apply(const F& f, const float* v) {
 // ---------------------------------------------------------------------------
 // flat: y[i] = f(x0[i or 0], x1[i or 0]) for i < n.
 
-constexpr int FLAT_U = 4;
+#ifndef OXI_FLAT_U
+#define OXI_FLAT_U 1
+#endif
+constexpr int FLAT_U = OXI_FLAT_U;  // float4s per thread in the flat kernels
 
-template <class F, int N>
+template <class F, int N, bool NTS>
 __global__ __launch_bounds__(BS) void map_flat_vec_k(F f, Plan<N> p, int64_t n, unsigned bcast_mask) {
   const int64_t n4 = n >> 2;
   const int64_t base = ((int64_t)blockIdx.x * BS * FLAT_U) + threadIdx.x;
@@ -60,7 +63,7 @@ __global__ __launch_bounds__(BS) void map_flat_vec_k(F f, Plan<N> p, int64_t n, 
 #pragma unroll
     for (int k = 0; k < N; ++k) {
       if (bcast_mask >> k & 1u) in[k][u] = f4{sc[k], sc[k], sc[k], sc[k]};
-      else if (i < n4) in[k][u] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p.x[k]) + i);
+      else if (i < n4) in[k][u] = ld_stream(reinterpret_cast<const f4*>(p.x[k]) + i);
     }
   }
 #pragma unroll
@@ -75,7 +78,7 @@ __global__ __launch_bounds__(BS) void map_flat_vec_k(F f, Plan<N> p, int64_t n, 
         for (int k = 0; k < N; ++k) v[k] = in[k][u][j];
         r[j] = apply<F, N>(f, v);
       }
-      __builtin_nontemporal_store(r, reinterpret_cast<f4*>(p.y) + i);
+      st_stream<NTS>(r, reinterpret_cast<f4*>(p.y) + i);
     }
   }
   // scalar tail (n % 4 elements) handled by the first block
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(BS) void map_tiled_k(F f, Plan<N> p, int jd, unsign
 // tiled, float4 flavour: same 64x64 tiles, every global access a 16-byte
 // vector (4 consecutive elements along the transposed input's unit-stride
 // dim when loading, along the output's innermost dim when storing).
-template <class F, int N>
+template <class F, int N, bool NTS>
 __global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, unsigned tmask, int64_t tiles_d,
                                                       int64_t tiles_j) {
   __shared__ float tile[N][T][T + 1];
@@ -241,7 +244,7 @@ __global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, un
       const int jj = (l % (T / 4)) * 4, dd = l / (T / 4);
       const int64_t gj = j0 + jj, gd = d0 + dd;
       f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (gj < nj && gd < nd) v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(q + gj + gd * p.st[k + 1][d]));
+      if (gj < nj && gd < nd) v = ld_stream(reinterpret_cast<const f4*>(q + gj + gd * p.st[k + 1][d]));
       tile[k][dd][jj] = v.x;
       tile[k][dd][jj + 1] = v.y;
       tile[k][dd][jj + 2] = v.z;
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, un
       for (int k = 0; k < N; ++k) v[k] = in[k][c];
       r[c] = apply<F, N>(f, v);
     }
-    __builtin_nontemporal_store(r, reinterpret_cast<f4*>(p.y + off[0] + gj * p.st[0][jd] + gd));
+    st_stream<NTS>(r, reinterpret_cast<f4*>(p.y + off[0] + gj * p.st[0][jd] + gd));
   }
 }
 
@@ -382,6 +385,7 @@ int launch_map(F f, const char* what, float* y, const int64_t* ys, const float* 
   int64_t n = 0;
   if (int rc = build_plan<N>(p, y, ys, xs, xst, shape, ndim, &n)) return rc;
   if (n == 0) return OXI_OK;
+  const bool nts = nt_stores(n * 4);
   OXI_CHECK_INIT();
   hipStream_t s = stream();
   const int d = p.ndim - 1;
@@ -403,7 +407,8 @@ int launch_map(F f, const char* what, float* y, const int64_t* ys, const float* 
     if (vec && n >= 4) {
       const int64_t n4 = n >> 2;
       const int64_t blocks = std::max<int64_t>(1, ceil_div(n4, (int64_t)BS * FLAT_U));
-      map_flat_vec_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, n, bmask);
+      if (nts) map_flat_vec_k<F, N, true><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, n, bmask);
+      else map_flat_vec_k<F, N, false><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, n, bmask);
     } else {
       const int64_t blocks = std::min<int64_t>(ceil_div(n, BS), (int64_t)cu_count() * 32);
       map_flat_k<F, N><<<dim3((unsigned)std::max<int64_t>(1, blocks)), dim3(BS), 0, s>>>(f, p, n, bmask);
@@ -472,7 +477,8 @@ int launch_map(F f, const char* what, float* y, const int64_t* ys, const float* 
           }
         }
         if (vec)
-          map_tiled_vec_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
+          if (nts) map_tiled_vec_k<F, N, true><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
+          else map_tiled_vec_k<F, N, false><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
         else
           map_tiled_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
         return check_launch(what);

@@ -43,7 +43,7 @@ __device__ __forceinline__ int64_t wrap_id(int64_t id, int64_t len, bool& ok) {
 // ---------------------------------------------------------------------------
 // Gather.
 
-template <bool VEC>
+template <bool VEC, bool NTS>
 __global__ __launch_bounds__(BS) void gather_k(const float* __restrict__ src, int64_t outer, int64_t len,
                                                int64_t inner, const int64_t* __restrict__ idx, int64_t n,
                                                float* __restrict__ out, int* __restrict__ guard) {
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(BS) void gather_k(const float* __restrict__ src, in
         v[r] = (r0 + r < rows && okr[r]) ? reinterpret_cast<const f4*>(src + srow[r])[c] : f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int r = 0; r < GRPB; ++r)
-        if (r0 + r < rows) __builtin_nontemporal_store(v[r], reinterpret_cast<f4*>(out + (r0 + r) * inner) + c);
+        if (r0 + r < rows) st_stream<NTS>(v[r], reinterpret_cast<f4*>(out + (r0 + r) * inner) + c);
     } else {
       float v[GRPB];
 #pragma unroll
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict_
 constexpr int SEG_U = 8;  // rows in flight per lane
 constexpr int ZR = 4;
 
-template <bool VEC>
+template <bool VEC, bool NTS>
 __global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, int64_t outer, int64_t n,
                                                   int64_t inner, int64_t len, const int* __restrict__ skeys,
                                                   const int* __restrict__ perm, float* __restrict__ grad,
@@ -330,8 +330,8 @@ __global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, i
       for (int64_t o = 0; o < outer; ++o) {
         float* dst = grad + (o * len + v) * inner;
         for (int64_t c = threadIdx.x; c < units; c += 256) {
-          if constexpr (VEC) __builtin_nontemporal_store(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + c);
-          else __builtin_nontemporal_store(0.f, dst + c);
+          if constexpr (VEC) st_stream<NTS>(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + c);
+          else st_stream<NTS>(0.f, dst + c);
         }
       }
     }
@@ -395,8 +395,8 @@ __global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, i
         const int pj = __builtin_amdgcn_readlane(my_pos, (i + j) & 63);  // uniform; used only if i + j < cnt
         if (i + j < cnt && active && (uint64_t)pj < (uint64_t)n) {
           const float* row = gb + (int64_t)pj * inner;
-          if constexpr (VEC) vals[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(row) + u);
-          else vals[j] = __builtin_nontemporal_load(row + u);
+          if constexpr (VEC) vals[j] = ld_stream(reinterpret_cast<const f4*>(row) + u);
+          else vals[j] = ld_stream(row + u);
         }
       }
 #pragma unroll
@@ -410,11 +410,15 @@ __global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, i
             const bool to_tail = tail_inc && q == cnt - 1;
             const bool to_head = !to_tail && head_inc && start == 0;
             float* dst;
-            if (to_tail) dst = part + (slot_tail * outer + o) * inner;
-            else if (to_head) dst = part + (slot_head * outer + o) * inner;
-            else dst = grad + (o * len + key) * inner;
-            if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
-            else dst[u] = acc;
+            if (to_tail || to_head) {  // partial slots are re-read by the fix-up: plain stores
+              dst = part + ((to_tail ? slot_tail : slot_head) * outer + o) * inner;
+              if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
+              else dst[u] = acc;
+            } else {
+              dst = grad + (o * len + key) * inner;
+              if constexpr (VEC) st_stream<NTS>(acc, reinterpret_cast<f4*>(dst) + u);
+              else st_stream<NTS>(acc, dst + u);
+            }
           }
           acc = V{};
           start = q + 1;
@@ -430,8 +434,8 @@ __global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, i
           const int pj = __builtin_amdgcn_readlane(nx_pos, (i + j) & 63);
           if (i + j < ext_len && active && (uint64_t)pj < (uint64_t)n) {
             const float* row = gb + (int64_t)pj * inner;
-            if constexpr (VEC) vals[j] = __builtin_nontemporal_load(reinterpret_cast<const f4*>(row) + u);
-            else vals[j] = __builtin_nontemporal_load(row + u);
+            if constexpr (VEC) vals[j] = ld_stream(reinterpret_cast<const f4*>(row) + u);
+            else vals[j] = ld_stream(row + u);
           }
         }
 #pragma unroll
@@ -440,8 +444,8 @@ __global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, i
       }
       if ((uint64_t)keyl < (uint64_t)len && active) {
         float* dst = grad + (o * len + keyl) * inner;
-        if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
-        else dst[u] = acc;
+        if constexpr (VEC) st_stream<NTS>(acc, reinterpret_cast<f4*>(dst) + u);
+        else st_stream<NTS>(acc, dst + u);
       }
     }
   }
@@ -581,8 +585,11 @@ int oxi_index_select(const float* src, int64_t outer, int64_t len, int64_t inner
     // (192 for a 768-float row), at most BS
     const int64_t units = vec ? inner / 4 : inner;
     const unsigned bt = (unsigned)std::min<int64_t>(BS, ceil_div(units, 64) * 64);
-    if (vec) gather_k<true><<<dim3((unsigned)blocks), dim3(bt), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
-    else gather_k<false><<<dim3((unsigned)blocks), dim3(bt), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
+    const bool nts = nt_stores(rows * inner * 4);
+    const dim3 gb((unsigned)blocks), tb(bt);
+    if (vec && nts) gather_k<true, true><<<gb, tb, 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
+    else if (vec) gather_k<true, false><<<gb, tb, 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
+    else gather_k<false, false><<<gb, tb, 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
   } else {
     const int64_t blocks = std::min<int64_t>(ceil_div(rows * inner, BS), (int64_t)cu_count() * 32);
     gather_elem_k<<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
@@ -651,14 +658,21 @@ int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inn
   if (int rc = check_launch("index_select_bwd/sort")) return rc;
   float* part = wsp.as<float>();
   const int64_t seg_blocks = ceil_div(stiles * chunks, 4);
+  // the rows of g stream through the cache while dW is written: decide on
+  // the launch's whole traffic, not on dW alone
+  const bool nts = nt_stores((total_out + outer * n * inner) * 4);
   const int64_t blocks = seg_blocks + ceil_div(len, ZR);
   if (blocks >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many rows");
-  if (vec)
-    seg_wave_k<true><<<(unsigned)blocks, 256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
-                                                      owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
+  const dim3 sg((unsigned)blocks), st256(256);
+  if (vec && nts)
+    seg_wave_k<true, true><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners, owner_count,
+                                                end_tile, st, stiles, (int)chunks, seg_blocks);
+  else if (vec)
+    seg_wave_k<true, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
+                                                 owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
   else
-    seg_wave_k<false><<<(unsigned)blocks, 256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
-                                                       owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
+    seg_wave_k<false, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
+                                                  owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
   if (int rc = check_launch("index_select_bwd/segments")) return rc;
   const unsigned fb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(stiles * c16, 4 * (int64_t)cu_count()));
   if (vec)

@@ -30,7 +30,7 @@ __device__ __forceinline__ float rsum(float v, float* lds) { return group_sum<TP
 // ---------------------------------------------------------------------------
 // Forward, register-resident rows.
 
-template <int TPR, int NV, bool LN>
+template <int TPR, int NV, bool LN, bool NTS>
 __global__ __launch_bounds__(BS) void norm_fwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  const float* __restrict__ b, float* __restrict__ y,
                                                  float* __restrict__ mean, float* __restrict__ rstd,
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(BS) void norm_fwd_k(const float* __restrict__ x, co
       xt.v[k] = o;
     }
   }
-  xt.store(y + row * H, h4, t);
+  xt.template store<NTS>(y + row * H, h4, t);
 }
 
 // Forward for any H / alignment: one block per row, rows re-read from cache.
@@ -123,15 +123,23 @@ __global__ __launch_bounds__(BS) void norm_fwd_loop_k(const float* __restrict__ 
 //
 // part (if not null): [2][gridDim.x][H] floats, dw partials then db partials.
 
-template <int TPR, int NV, int MODE, bool LN>
-__global__ __launch_bounds__(BS) void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
+// Threads per backward block: one-wave rows run 16 to a block (one block per
+// CU: 16 waves in flight, one partial row per CU), or 8 to a block (two
+// blocks per CU) when 4 float4s per lane would not fit the registers of 16;
+// wider rows 1 per block.
+template <int TPR, int NV>
+constexpr int bwd_threads() { return TPR == 64 ? (NV <= 3 ? 1024 : 512) : BS; }
+
+template <int TPR, int NV, int MODE, bool LN, bool NTS>
+__global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  const float* __restrict__ mean, const float* __restrict__ rstd,
                                                  const float* __restrict__ g, float* __restrict__ dx,
                                                  float* __restrict__ part, int64_t rows, int H) {
-  constexpr int GPB = BS / TPR;
+  constexpr int NT = bwd_threads<TPR, NV>();
+  constexpr int GPB = NT / TPR;
   constexpr int ROWF = TPR * NV * 4;  // floats a group covers
   __shared__ float lds[2 * (BS / 64)];
-  __shared__ float comb[GPB > 1 ? 2 * GPB * ROWF : 1];
+  __shared__ float comb[GPB > 1 ? GPB * ROWF : 1];
   const int t = threadIdx.x % TPR;
   const int gi = threadIdx.x / TPR;
   const int h4 = H >> 2;
@@ -143,19 +151,37 @@ __global__ __launch_bounds__(BS) void norm_bwd_k(const float* __restrict__ x, co
 #pragma unroll
   for (int k = 0; k < NV; ++k) { pdw[k] = zero; pdb[k] = zero; }
 
+  // weights (padding lanes: 0); cached, re-read per row to save registers
+  auto wv_at = [&](int k) -> f4 {
+    const int c = k * TPR + t;
+    return (c < h4) ? (w ? w4[c] : f4{1.f, 1.f, 1.f, 1.f}) : zero;
+  };
+  // rows are double-buffered: the next row's x, g and statistics are in
+  // flight while the current row is reduced and stored
   const int64_t ngroups = (int64_t)gridDim.x * GPB;
-  for (int64_t row = (int64_t)blockIdx.x * GPB + gi; row < rows; row += ngroups) {
-    RowTile<TPR, NV> xt, gt;
+  int64_t row = (int64_t)blockIdx.x * GPB + gi;
+  RowTile<TPR, NV> xt, gt;
+  float inv = 0.f, mu = 0.f;
+  if (row < rows) {
     xt.load(x + row * H, h4, t);
     gt.load(g + row * H, h4, t);
-    const float inv = rstd[row];
-    const float mu = LN ? mean[row] : 0.f;
-    // xhat = (x - mu) * inv ; gw = g * w   (padding lanes stay 0: w pad read as 0)
-    f4 wv[NV];
+    inv = rstd[row];
+    if constexpr (LN) mu = mean[row];
+  }
+  while (row < rows) {
+    const int64_t nrow = row + ngroups;
+    RowTile<TPR, NV> xn, gn;
+    float ninv = 0.f, nmu = 0.f;
+    if (nrow < rows) {
+      xn.load(x + nrow * H, h4, t);
+      gn.load(g + nrow * H, h4, t);
+      ninv = rstd[nrow];
+      if constexpr (LN) nmu = mean[nrow];
+    }
+    // xhat = (x - mu) * inv ; gw = g * w   (padding lanes stay 0)
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = k * TPR + t;
-      wv[k] = (w && c < h4) ? w4[c] : ((c < h4) ? f4{1.f, 1.f, 1.f, 1.f} : zero);
       f4 xh = LN ? (xt.v[k] - mu) * inv : xt.v[k] * inv;
       if (c >= h4) xh = zero;
       xt.v[k] = xh;  // xt now holds xhat
@@ -168,7 +194,7 @@ __global__ __launch_bounds__(BS) void norm_bwd_k(const float* __restrict__ x, co
         float s = 0.f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-          gt.v[k] = (gt.v[k] * wv[k]) * inv;
+          gt.v[k] = (gt.v[k] * wv_at(k)) * inv;
           s += (gt.v[k].x + gt.v[k].y) + (gt.v[k].z + gt.v[k].w);
         }
         if constexpr (LN) {
@@ -181,7 +207,7 @@ __global__ __launch_bounds__(BS) void norm_bwd_k(const float* __restrict__ x, co
         float sa = 0.f, sb = 0.f;
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
-          gt.v[k] = gt.v[k] * wv[k];
+          gt.v[k] = gt.v[k] * wv_at(k);
           const f4 p = gt.v[k] * xt.v[k];
           sb += (p.x + p.y) + (p.z + p.w);
           sa += (gt.v[k].x + gt.v[k].y) + (gt.v[k].z + gt.v[k].w);
@@ -192,8 +218,13 @@ __global__ __launch_bounds__(BS) void norm_bwd_k(const float* __restrict__ x, co
 #pragma unroll
         for (int k = 0; k < NV; ++k) gt.v[k] = ((gt.v[k] - a) - xt.v[k] * bcoef) * inv;
       }
-      gt.store(dx + row * H, h4, t);
+      gt.template store<NTS>(dx + row * H, h4, t);
     }
+    xt = xn;
+    gt = gn;
+    inv = ninv;
+    mu = nmu;
+    row = nrow;
   }
   if (!part) return;
   float* pw = part + (int64_t)blockIdx.x * H;
@@ -208,23 +239,21 @@ __global__ __launch_bounds__(BS) void norm_bwd_k(const float* __restrict__ x, co
       }
     }
   } else {
-    // combine the GPB groups of this block in fixed group order
+    // combine the GPB groups of this block in fixed group order, one plane
+    // (dw, then db) at a time through the same LDS buffer
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int c = k * TPR + t;
-      reinterpret_cast<f4*>(comb + gi * ROWF)[c] = pdw[k];
-      reinterpret_cast<f4*>(comb + (GPB + gi) * ROWF)[c] = pdb[k];
-    }
-    __syncthreads();
-    for (int c = threadIdx.x; c < H; c += BS) {
-      float sw = comb[c], sb = comb[GPB * ROWF + c];
+    for (int plane = 0; plane < (LN ? 2 : 1); ++plane) {
 #pragma unroll
-      for (int q = 1; q < GPB; ++q) {
-        sw += comb[q * ROWF + c];
-        sb += comb[(GPB + q) * ROWF + c];
+      for (int k = 0; k < NV; ++k) reinterpret_cast<f4*>(comb + gi * ROWF)[k * TPR + t] = plane ? pdb[k] : pdw[k];
+      __syncthreads();
+      float* dst = plane ? pb : pw;
+      for (int c = threadIdx.x; c < H; c += NT) {
+        float sum = comb[c];
+#pragma unroll
+        for (int q = 1; q < GPB; ++q) sum += comb[q * ROWF + c];
+        dst[c] = sum;
       }
-      pw[c] = sw;
-      if (LN) pb[c] = sb;
+      __syncthreads();
     }
   }
 }
@@ -282,9 +311,10 @@ __global__ __launch_bounds__(BS) void norm_bwd_loop_k(const float* __restrict__ 
 
 // out[c] = sum over partial rows b (fixed order, float64) of part[b][c].
 // A block owns 64 columns; its FIN_W waves each sum the rows b = s, s+FIN_W,
-// ... of one slice s, then the slice sums are added in slice order.
-// blockIdx.y selects the dw (0) or db (1) plane.
+// ... of one slice s (FIN_U loads in flight), then the slice sums are added
+// in slice order. blockIdx.y selects the dw (0) or db (1) plane.
 constexpr int FIN_W = 16;
+constexpr int FIN_U = 16;
 
 __global__ __launch_bounds__(64 * FIN_W) void col_finish_k(const float* __restrict__ part, int nb, int H,
                                                            float* __restrict__ out0, float* __restrict__ out1) {
@@ -294,10 +324,15 @@ __global__ __launch_bounds__(64 * FIN_W) void col_finish_k(const float* __restri
   const int lane = threadIdx.x & 63;
   const int slice = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
+  const int cc = min(c, H - 1);  // in range: loads issue together
   double acc = 0.0;
-  if (c < H) {
-#pragma unroll 4
-    for (int b = slice; b < nb; b += FIN_W) acc += (double)p[(int64_t)b * H + c];
+  for (int b0 = slice; b0 < nb; b0 += FIN_W * FIN_U) {
+    float v[FIN_U];
+#pragma unroll
+    for (int q = 0; q < FIN_U; ++q) v[q] = p[(int64_t)min(b0 + FIN_W * q, nb - 1) * H + cc];
+#pragma unroll
+    for (int q = 0; q < FIN_U; ++q)
+      if (b0 + FIN_W * q < nb) acc += (double)v[q];
   }
   __shared__ double s[FIN_W][64];
   s[slice][lane] = acc;
@@ -332,17 +367,14 @@ int pick_cfg(int64_t h4) {
   return 0;
 }
 
-template <bool LN>
-int launch_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
-               int64_t rows, int64_t H, float eps) {
-  hipStream_t s = stream();
-  const int cfg = vec_ok(H, {x, w, b, y}) ? pick_cfg(H / 4) : 0;
-  const int h = (int)H;
-#define OXI_FWD(TPR, NV)                                                                              \
-  case TPR * 10 + NV:                                                                                 \
-    norm_fwd_k<TPR, NV, LN><<<dim3((unsigned)ceil_div(rows, BS / TPR)), dim3(BS), 0, s>>>(x, w, b, y, \
-                                                                                        mean, rstd,   \
-                                                                                        rows, h, eps); \
+template <bool LN, bool NTS>
+void launch_fwd_cfg(int cfg, hipStream_t s, const float* x, const float* w, const float* b, float* y, float* mean,
+                    float* rstd, int64_t rows, int h, float eps) {
+#define OXI_FWD(TPR, NV)                                                                                   \
+  case TPR * 10 + NV:                                                                                      \
+    norm_fwd_k<TPR, NV, LN, NTS><<<dim3((unsigned)ceil_div(rows, BS / TPR)), dim3(BS), 0, s>>>(x, w, b, y, \
+                                                                                             mean, rstd,   \
+                                                                                             rows, h, eps); \
     break;
   switch (cfg) {
     OXI_FWD(64, 1)
@@ -356,32 +388,26 @@ int launch_fwd(const float* x, const float* w, const float* b, float* y, float* 
       norm_fwd_loop_k<LN><<<dim3((unsigned)rows), dim3(BS), 0, s>>>(x, w, b, y, mean, rstd, rows, h, eps);
   }
 #undef OXI_FWD
+}
+
+template <bool LN>
+int launch_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
+               int64_t rows, int64_t H, float eps) {
+  hipStream_t s = stream();
+  const int cfg = vec_ok(H, {x, w, b, y}) ? pick_cfg(H / 4) : 0;
+  const int h = (int)H;
+  if (nt_stores(rows * H * 4)) launch_fwd_cfg<LN, true>(cfg, s, x, w, b, y, mean, rstd, rows, h, eps);
+  else launch_fwd_cfg<LN, false>(cfg, s, x, w, b, y, mean, rstd, rows, h, eps);
   return check_launch(LN ? "layer_norm_fwd" : "rms_norm_fwd");
 }
 
-template <bool LN, int MODE>
-int launch_bwd(const float* x, const float* w, const float* mean, const float* rstd, const float* g,
-               float* dx, float* dw, float* db, int64_t rows, int64_t H) {
-  hipStream_t s = stream();
-  const bool need_part = dw || (LN && db);
-  const int cfg = vec_ok(H, {x, w, g, dx}) ? pick_cfg(H / 4) : 0;
-  const int tpr = cfg ? cfg / 10 : BS;
-  const int gpb = BS / tpr;
-  // Blocks: enough to fill the chip, few enough that the partial rows stay
-  // a small fraction of the row traffic.
-  int64_t nblk = ceil_div(rows, gpb);
-  const int64_t cap = (int64_t)cu_count() * (tpr >= 256 ? 2 : 2);
-  if (need_part && nblk > cap) nblk = cap;
-  if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
-  if (nblk < 1) nblk = 1;
-  Workspace ws(need_part ? sizeof(float) * 2 * (size_t)nblk * (size_t)H : 0);
-  if (need_part && !ws.p) return OXI_OTHER;
-  float* part = ws.as<float>();
-  const int h = (int)H;
-#define OXI_BWD(TPR, NV)                                                                              \
-  case TPR * 10 + NV:                                                                                 \
-    norm_bwd_k<TPR, NV, MODE, LN><<<dim3((unsigned)nblk), dim3(BS), 0, s>>>(x, w, mean, rstd, g, dx,  \
-                                                                           part, rows, h);            \
+template <bool LN, int MODE, bool NTS>
+void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x, const float* w, const float* mean,
+                    const float* rstd, const float* g, float* dx, float* part, int64_t rows, int h) {
+#define OXI_BWD(TPR, NV)                                                                                   \
+  case TPR * 10 + NV:                                                                                      \
+    norm_bwd_k<TPR, NV, MODE, LN, NTS><<<dim3((unsigned)nblk), dim3(nt), 0, s>>>(x, w, mean, rstd, g, dx,  \
+                                                                                part, rows, h);            \
     break;
   switch (cfg) {
     OXI_BWD(64, 1)
@@ -395,6 +421,30 @@ int launch_bwd(const float* x, const float* w, const float* mean, const float* r
       norm_bwd_loop_k<MODE, LN><<<dim3((unsigned)nblk), dim3(BS), 0, s>>>(x, w, mean, rstd, g, dx, part, rows, h);
   }
 #undef OXI_BWD
+}
+
+template <bool LN, int MODE>
+int launch_bwd(const float* x, const float* w, const float* mean, const float* rstd, const float* g,
+               float* dx, float* dw, float* db, int64_t rows, int64_t H) {
+  hipStream_t s = stream();
+  const bool need_part = dw || (LN && db);
+  const int cfg = vec_ok(H, {x, w, g, dx}) ? pick_cfg(H / 4) : 0;
+  const int tpr = cfg ? cfg / 10 : BS;
+  const int nt = tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : BS;  // bwd_threads<TPR, NV>()
+  const int gpb = nt / tpr;
+  // Blocks: enough to fill the chip, few enough that the partial rows stay
+  // a small fraction of the row traffic.
+  int64_t nblk = ceil_div(rows, gpb);
+  const int64_t cap = (int64_t)cu_count() * (nt == 1024 ? 1 : 2);
+  if (need_part && nblk > cap) nblk = cap;
+  if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
+  if (nblk < 1) nblk = 1;
+  Workspace ws(need_part ? sizeof(float) * 2 * (size_t)nblk * (size_t)H : 0);
+  if (need_part && !ws.p) return OXI_OTHER;
+  float* part = ws.as<float>();
+  const int h = (int)H;
+  if (nt_stores(rows * H * 4)) launch_bwd_cfg<LN, MODE, true>(cfg, s, nblk, nt, x, w, mean, rstd, g, dx, part, rows, h);
+  else launch_bwd_cfg<LN, MODE, false>(cfg, s, nblk, nt, x, w, mean, rstd, g, dx, part, rows, h);
   int rc = check_launch(LN ? "layer_norm_bwd" : "rms_norm_bwd");
   if (rc != OXI_OK) return rc;
   if (need_part) {

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(BS) void reduce_strided_vec_k(const float* __restri
     else a = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
     for (int64_t k = 0; k < p.len; ++k) {
-      const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(s + k * p.rst));
+      const f4 v = ld_stream(reinterpret_cast<const f4*>(s + k * p.rst));
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         if constexpr (K == OXI_REDUCE_SUM || K == OXI_REDUCE_MEAN) a[c] += v[c];

@@ -66,7 +66,7 @@ __device__ __forceinline__ void group_online(Online& o, float* lds) {
 // ---------------------------------------------------------------------------
 // Last-dim kernels, register-resident rows.
 
-template <int TPR, int NV, bool LOG>
+template <int TPR, int NV, bool LOG, bool NTS>
 __global__ __launch_bounds__(BS) void sm_fwd_k(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int H) {
   constexpr int GPB = BS / TPR;
   __shared__ float lds[2 * (BS / 64)];
@@ -100,10 +100,10 @@ __global__ __launch_bounds__(BS) void sm_fwd_k(const float* __restrict__ x, floa
 #pragma unroll
     for (int k = 0; k < NV; ++k) xt.v[k] = xt.v[k] / s;
   }
-  xt.store(y + row * H, h4, t);
+  xt.template store<NTS>(y + row * H, h4, t);
 }
 
-template <int TPR, int NV, bool LOG>
+template <int TPR, int NV, bool LOG, bool NTS>
 __global__ __launch_bounds__(BS) void sm_bwd_k(const float* __restrict__ y, const float* __restrict__ g,
                                                float* __restrict__ dx, int64_t rows, int H) {
   constexpr int GPB = BS / TPR;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(BS) void sm_bwd_k(const float* __restrict__ y, cons
     if constexpr (LOG) gt.v[k] = gt.v[k] - exp4(yt.v[k]) * s;
     else gt.v[k] = yt.v[k] * (gt.v[k] - s);
   }
-  gt.store(dx + row * H, h4, t);
+  gt.template store<NTS>(dx + row * H, h4, t);
 }
 
 // Last-dim kernels for any length / alignment: one block per row, two passes.
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logi
     for (; c + (CE_U - 1) * CE_BS < c4; c += CE_U * CE_BS) {
       f4 v[CE_U];
 #pragma unroll
-      for (int u = 0; u < CE_U; ++u) v[u] = __builtin_nontemporal_load(p + c + u * CE_BS);
+      for (int u = 0; u < CE_U; ++u) v[u] = ld_stream(p + c + u * CE_BS);
       float cm = max4(v[0]);
 #pragma unroll
       for (int u = 1; u < CE_U; ++u) cm = fmaxf(cm, max4(v[u]));
@@ -268,6 +268,7 @@ __global__ __launch_bounds__(1024) void ce_mean_k(const float* __restrict__ pick
 }
 
 // dlogits = (exp(x - lse) - onehot) * (g / n). Grid: (column blocks, rows).
+template <bool NTS>
 __global__ __launch_bounds__(CE_BS) void ce_bwd_k(const float* __restrict__ logits, const int64_t* __restrict__ targets,
                                                   const float* __restrict__ lse, const float* __restrict__ gloss,
                                                   float* __restrict__ dlogits, int64_t n, int C, int vec) {
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(CE_BS) void ce_bwd_k(const float* __restrict__ logi
 #pragma unroll
     for (int u = 0; u < CE_U; ++u) {
       const int c = c0 + u * CE_BS;
-      if (c < c4) v[u] = __builtin_nontemporal_load(p + c);
+      if (c < c4) v[u] = ld_stream(p + c);
     }
 #pragma unroll
     for (int u = 0; u < CE_U; ++u) {
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(CE_BS) void ce_bwd_k(const float* __restrict__ logi
           else if (j == 2) e.z -= 1.f;
           else e.w -= 1.f;
         }
-        __builtin_nontemporal_store(e * scale, q + c);
+        st_stream<NTS>(e * scale, q + c);
       }
     }
   } else {
@@ -356,9 +357,11 @@ int launch_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inn
   if (inner == 1) {
     const int cfg = (len % 4 == 0 && aligned16({x, y})) ? pick_cfg(len / 4) : 0;
     const int h = (int)len;
-#define OXI_SMF(TPR, NV)                                                                                  \
-  case TPR * 10 + NV:                                                                                     \
-    sm_fwd_k<TPR, NV, LOG><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(x, y, outer, h); \
+    const bool nts = nt_stores(outer * len * 4);
+#define OXI_SMF(TPR, NV)                                                                                            \
+  case TPR * 10 + NV:                                                                                               \
+    if (nts) sm_fwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(x, y, outer, h);  \
+    else sm_fwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(x, y, outer, h);     \
     break;
     switch (cfg) {
       OXI_SMF(64, 1)
@@ -384,9 +387,11 @@ int launch_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t
   if (inner == 1) {
     const int cfg = (len % 4 == 0 && aligned16({y, g, dx})) ? pick_cfg(len / 4) : 0;
     const int h = (int)len;
+    const bool nts = nt_stores(outer * len * 4);
 #define OXI_SMB(TPR, NV)                                                                                        \
   case TPR * 10 + NV:                                                                                           \
-    sm_bwd_k<TPR, NV, LOG><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(y, g, dx, outer, h); \
+    if (nts) sm_bwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(y, g, dx, outer, h);  \
+    else sm_bwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(y, g, dx, outer, h);     \
     break;
     switch (cfg) {
       OXI_SMB(64, 1)
@@ -472,17 +477,23 @@ int oxi_cross_entropy_bwd(const float* logits, const int64_t* targets, const flo
   const int vec = (c % 4 == 0 && aligned16({logits, dlogits})) ? 1 : 0;
   const int64_t units = vec ? c / 4 : c;
   const unsigned gx = (unsigned)ceil_div(units, CE_BS * CE_U);
+  const bool nts = nt_stores(n * c * 4);
   if (n > 65535) {
     // grid.y is limited; launch row slabs
     for (int64_t r0 = 0; r0 < n; r0 += 65535) {
       const int64_t nr = (n - r0) < 65535 ? (n - r0) : 65535;
-      ce_bwd_k<<<dim3(gx, (unsigned)nr), dim3(CE_BS), 0, stream()>>>(logits + r0 * c, targets + r0, lse + r0, gloss,
-                                                                     dlogits + r0 * c, n, (int)c, vec);
+      if (nts)
+        ce_bwd_k<true><<<dim3(gx, (unsigned)nr), dim3(CE_BS), 0, stream()>>>(logits + r0 * c, targets + r0, lse + r0,
+                                                                             gloss, dlogits + r0 * c, n, (int)c, vec);
+      else
+        ce_bwd_k<false><<<dim3(gx, (unsigned)nr), dim3(CE_BS), 0, stream()>>>(logits + r0 * c, targets + r0, lse + r0,
+                                                                              gloss, dlogits + r0 * c, n, (int)c, vec);
       if (int rc = check_launch("cross_entropy_bwd")) return rc;
     }
     return OXI_OK;
   }
-  ce_bwd_k<<<dim3(gx, (unsigned)n), dim3(CE_BS), 0, stream()>>>(logits, targets, lse, gloss, dlogits, n, (int)c, vec);
+  if (nts) ce_bwd_k<true><<<dim3(gx, (unsigned)n), dim3(CE_BS), 0, stream()>>>(logits, targets, lse, gloss, dlogits, n, (int)c, vec);
+  else ce_bwd_k<false><<<dim3(gx, (unsigned)n), dim3(CE_BS), 0, stream()>>>(logits, targets, lse, gloss, dlogits, n, (int)c, vec);
   return check_launch("cross_entropy_bwd");
 }
 
