@@ -209,46 +209,60 @@ __global__ __launch_bounds__(BS) void map_tiled_k(F f, Plan<N> p, int jd, unsign
 
 // tiled, float4 flavour: same 64x64 tiles, every global access a 16-byte
 // vector (4 consecutive elements along the transposed input's unit-stride
-// dim when loading, along the output's innermost dim when storing).
-template <class F, int N, bool NTS>
-__global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, unsigned tmask, int64_t tiles_d,
-                                                      int64_t tiles_j) {
-  __shared__ float tile[N][T][T + 1];
+// dim when loading, along the output's innermost dim when storing). TM (the
+// transposed-input mask) is a template parameter so that LDS holds tiles for
+// the transposed inputs only; block indices are decoded in 32-bit arithmetic.
+template <int N, unsigned TM>
+constexpr int tile_slot(int k) {
+  int s = 0;
+  for (int q = 0; q < k; ++q) s += (TM >> q) & 1u;
+  return s;
+}
+
+template <class F, int N, unsigned TM, bool NTS>
+__global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, unsigned tiles_d, unsigned tiles_j) {
+  constexpr int NTR = tile_slot<N, TM>(N);  // number of transposed inputs
+  __shared__ float tile[NTR][T][T + 1];
   const int d = p.ndim - 1;
-  int64_t b = blockIdx.x;
-  const int64_t td = b % tiles_d;
+  unsigned b = blockIdx.x;
+  const unsigned td = b % tiles_d;
   b /= tiles_d;
-  const int64_t tj = b % tiles_j;
+  const unsigned tj = b % tiles_j;
   b /= tiles_j;
   int64_t off[N + 1];
 #pragma unroll
   for (int k = 0; k <= N; ++k) off[k] = 0;
   for (int q = p.ndim - 2; q >= 0; --q) {
     if (q == jd) continue;
-    const int64_t c = b % p.shape[q];
-    b /= p.shape[q];
+    const unsigned sz = (unsigned)p.shape[q];
+    const unsigned c = b % sz;
+    b /= sz;
 #pragma unroll
-    for (int k = 0; k <= N; ++k) off[k] += c * p.st[k][q];
+    for (int k = 0; k <= N; ++k) off[k] += (int64_t)c * p.st[k][q];
   }
-  const int64_t j0 = tj * T, d0 = td * T;
-  const int64_t nj = p.shape[jd], nd = p.shape[d];
+  const int j0 = (int)tj * T, d0 = (int)td * T;
+  const int nj = (int)p.shape[jd], nd = (int)p.shape[d];
   const int t = threadIdx.x;
   // loads of transposed inputs: 16 lanes cover 64 consecutive j of one d
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    if (!(tmask >> k & 1u)) continue;
+    if constexpr (true) {
+      if (!((TM >> k) & 1u)) continue;
+    }
     const float* q = p.x[k] + off[k + 1];
+    const int64_t sd = p.st[k + 1][d];
 #pragma unroll
     for (int i = 0; i < (T * T / 4) / BS; ++i) {
       const int l = i * BS + t;
       const int jj = (l % (T / 4)) * 4, dd = l / (T / 4);
-      const int64_t gj = j0 + jj, gd = d0 + dd;
+      const int gj = j0 + jj, gd = d0 + dd;
       f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (gj < nj && gd < nd) v = ld_stream(reinterpret_cast<const f4*>(q + gj + gd * p.st[k + 1][d]));
-      tile[k][dd][jj] = v.x;
-      tile[k][dd][jj + 1] = v.y;
-      tile[k][dd][jj + 2] = v.z;
-      tile[k][dd][jj + 3] = v.w;
+      if (gj < nj && gd < nd) v = ld_stream(reinterpret_cast<const f4*>(q + gj + gd * sd));
+      float* row = &tile[tile_slot<N, TM>(k)][dd][jj];
+      row[0] = v.x;
+      row[1] = v.y;
+      row[2] = v.z;
+      row[3] = v.w;
     }
   }
   __syncthreads();
@@ -257,15 +271,16 @@ __global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, un
   for (int i = 0; i < (T * T / 4) / BS; ++i) {
     const int l = i * BS + t;
     const int dd = (l % (T / 4)) * 4, jj = l / (T / 4);
-    const int64_t gj = j0 + jj, gd = d0 + dd;
+    const int gj = j0 + jj, gd = d0 + dd;
     if (gj >= nj || gd >= nd) continue;
     f4 in[N];
 #pragma unroll
     for (int k = 0; k < N; ++k) {
-      if (tmask >> k & 1u) {
-        in[k] = f4{tile[k][dd][jj], tile[k][dd + 1][jj], tile[k][dd + 2][jj], tile[k][dd + 3][jj]};
+      if ((TM >> k) & 1u) {
+        const int ts = tile_slot<N, TM>(k);
+        in[k] = f4{tile[ts][dd][jj], tile[ts][dd + 1][jj], tile[ts][dd + 2][jj], tile[ts][dd + 3][jj]};
       } else {
-        const float* q = p.x[k] + off[k + 1] + gj * p.st[k + 1][jd];
+        const float* q = p.x[k] + off[k + 1] + (int64_t)gj * p.st[k + 1][jd];
         if (p.st[k + 1][d] == 0) in[k] = f4{q[0], q[0], q[0], q[0]};
         else in[k] = *reinterpret_cast<const f4*>(q + gd);
       }
@@ -278,8 +293,15 @@ __global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, un
       for (int k = 0; k < N; ++k) v[k] = in[k][c];
       r[c] = apply<F, N>(f, v);
     }
-    st_stream<NTS>(r, reinterpret_cast<f4*>(p.y + off[0] + gj * p.st[0][jd] + gd));
+    st_stream<NTS>(r, reinterpret_cast<f4*>(p.y + off[0] + (int64_t)gj * p.st[0][jd] + gd));
   }
+}
+
+template <class F, int N, unsigned TM>
+void launch_tiled_vec(F f, const Plan<N>& p, int jd, unsigned blocks, unsigned tiles_d, unsigned tiles_j, bool nts,
+                      hipStream_t s) {
+  if (nts) map_tiled_vec_k<F, N, TM, true><<<dim3(blocks), dim3(BS), 0, s>>>(f, p, jd, tiles_d, tiles_j);
+  else map_tiled_vec_k<F, N, TM, false><<<dim3(blocks), dim3(BS), 0, s>>>(f, p, jd, tiles_d, tiles_j);
 }
 
 // ---------------------------------------------------------------------------
@@ -476,10 +498,17 @@ int launch_map(F f, const char* what, float* y, const int64_t* ys, const float* 
             if (p.st[k + 1][q] % 4) vec = false;
           }
         }
-        if (vec)
-          if (nts) map_tiled_vec_k<F, N, true><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
-          else map_tiled_vec_k<F, N, false><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
-        else
+        // 32-bit block decode: every dim and the block count stay below 2^31
+        for (int q = 0; q < p.ndim && vec; ++q)
+          if (p.shape[q] >= ((int64_t)1 << 31)) vec = false;
+        if (vec) {
+          const unsigned nb = (unsigned)blocks, ntd = (unsigned)tiles_d, ntj = (unsigned)tiles_j;
+          if (tmask == 1u) launch_tiled_vec<F, N, 1u>(f, p, jd, nb, ntd, ntj, nts, s);
+          else if constexpr (N == 2) {
+            if (tmask == 2u) launch_tiled_vec<F, N, 2u>(f, p, jd, nb, ntd, ntj, nts, s);
+            else launch_tiled_vec<F, N, 3u>(f, p, jd, nb, ntd, ntj, nts, s);
+          }
+        } else
           map_tiled_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
         return check_launch(what);
       }

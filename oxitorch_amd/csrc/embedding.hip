@@ -32,7 +32,10 @@ namespace oxi {
 namespace {
 
 constexpr int BS = 256;
-constexpr int GRPB = 8;       // rows per gather step
+#ifndef OXI_GRPB
+#define OXI_GRPB 2
+#endif
+constexpr int GRPB = OXI_GRPB;  // rows per gather block
 
 __device__ __forceinline__ int64_t wrap_id(int64_t id, int64_t len, bool& ok) {
   if (id < 0) id += len;
@@ -122,10 +125,12 @@ constexpr int SCAN_REG = 64;     // table rows one thread holds at a time
 constexpr int SELF_SCAN_MAX = 256;  // tiles up to which each scatter block scans the table itself
 constexpr int SEEN = 1024;       // LDS filter of recently flagged keys
 
-__device__ __forceinline__ int key_of(const int64_t* __restrict__ idx, int64_t p, int64_t len, int* guard) {
+// Key of a raw id (no memory access: callers load a batch of ids first, so
+// that the loads are in flight together, then convert and report once).
+__device__ __forceinline__ int key_from(int64_t raw, int64_t len, bool& bad) {
   bool ok;
-  const int64_t id = wrap_id(idx[p], len, ok);
-  if (!ok) atomicOr(guard, 1);
+  const int64_t id = wrap_id(raw, len, ok);
+  bad |= !ok;
   return ok ? (int)id : (int)len;
 }
 
@@ -179,11 +184,20 @@ __global__ __launch_bounds__(SBS) void sort_hist_k(const int64_t* __restrict__ i
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * (SBS * IPT);
   int k[IPT];
+  if constexpr (FROM_IDX) {
+    int64_t raw[IPT];
 #pragma unroll
-  for (int i = 0; i < IPT; ++i) {
-    const int64_t p = base + i * SBS + t;
-    k[i] = -1;
-    if (p < n) k[i] = FROM_IDX ? key_of(idx, p, len, guard) : keys[p];
+    for (int i = 0; i < IPT; ++i) raw[i] = idx[min<int64_t>(base + i * SBS + t, n - 1)];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) k[i] = (base + i * SBS + t < n) ? key_from(raw[i], len, bad) : -1;
+    if (bad) atomicOr(guard, 1);
+  } else {
+#pragma unroll
+    for (int i = 0; i < IPT; ++i) k[i] = keys[min<int64_t>(base + i * SBS + t, n - 1)];
+#pragma unroll
+    for (int i = 0; i < IPT; ++i)
+      if (base + i * SBS + t >= n) k[i] = -1;
   }
 #pragma unroll
   for (int i = 0; i < IPT; ++i)
@@ -209,7 +223,10 @@ __global__ __launch_bounds__(SBS) void sort_offsets_k(int* tab, int ntiles) {
   }
 }
 
-template <int IPT, bool FROM_IDX, bool SELF_SCAN>
+// How a scatter block finds its 256 output offsets.
+enum { OFFS_TABLE = 0, OFFS_SCAN_COUNTS = 1 };
+
+template <int IPT, bool FROM_IDX, int OFFS>
 __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict__ idx, const int* __restrict__ keys,
                                                       const int* __restrict__ vals, int64_t n, int64_t len, int shift,
                                                       int ntiles, const int* __restrict__ tab,
@@ -223,17 +240,27 @@ __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict_
   const int64_t tile0 = (int64_t)blockIdx.x * (SBS * IPT);
   // all of this thread's elements up front: one load latency for the tile
   int kk[IPT], vv[IPT];
+  if constexpr (FROM_IDX) {
+    int64_t raw[IPT];
 #pragma unroll
-  for (int r = 0; r < IPT; ++r) {
-    const int64_t p = tile0 + r * SBS + t;
-    kk[r] = 0;
-    vv[r] = 0;
-    if (p < n) {
-      kk[r] = FROM_IDX ? key_of(idx, p, len, guard) : keys[p];
-      vv[r] = FROM_IDX ? (int)p : vals[p];
+    for (int r = 0; r < IPT; ++r) raw[r] = idx[min<int64_t>(tile0 + r * SBS + t, n - 1)];
+    bool bad = false;
+#pragma unroll
+    for (int r = 0; r < IPT; ++r) {
+      const int64_t p = tile0 + r * SBS + t;
+      kk[r] = p < n ? key_from(raw[r], len, bad) : 0;
+      vv[r] = (int)p;
+    }
+    if (bad) atomicOr(guard, 1);
+  } else {
+#pragma unroll
+    for (int r = 0; r < IPT; ++r) {
+      const int64_t pc = min<int64_t>(tile0 + r * SBS + t, n - 1);
+      kk[r] = keys[pc];
+      vv[r] = vals[pc];
     }
   }
-  if constexpr (SELF_SCAN) {
+  if constexpr (OFFS == OFFS_SCAN_COUNTS) {
     int total, before;
     column_sums(tab, ntiles, (int)blockIdx.x, total, before);
     base[t] = block_excl_scan256(total, ws) + before;
@@ -534,21 +561,21 @@ __global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t n, int
 }
 
 template <int IPT>
-void sort_pass(hipStream_t s, int ps, int passes, int64_t n, int64_t len, int ntiles, const int64_t* idx,
-               const int* ka, const int* va, int* kb, int* vb, int* tab, int* present, int* owner_count) {
-  (void)passes;
+void sort_pass(hipStream_t s, int ps, int64_t n, int64_t len, int ntiles, const int64_t* idx, const int* ka,
+               const int* va, int* kb, int* vb, int* tab, int* present, int* owner_count) {
   const int shift = 8 * ps;
   const unsigned nb = (unsigned)ntiles;
+  int* gd = guard_flag();
   const bool self = ntiles <= SELF_SCAN_MAX;
-  if (ps == 0) sort_hist_k<IPT, true><<<nb, SBS, 0, s>>>(idx, nullptr, n, len, shift, tab, present, owner_count, guard_flag());
-  else sort_hist_k<IPT, false><<<nb, SBS, 0, s>>>(nullptr, ka, n, len, shift, tab, nullptr, nullptr, guard_flag());
+  if (ps == 0) sort_hist_k<IPT, true><<<nb, SBS, 0, s>>>(idx, nullptr, n, len, shift, tab, present, owner_count, gd);
+  else sort_hist_k<IPT, false><<<nb, SBS, 0, s>>>(nullptr, ka, n, len, shift, tab, nullptr, nullptr, gd);
   if (!self) sort_offsets_k<<<1, SBS, 0, s>>>(tab, ntiles);
   if (ps == 0) {
-    if (self) sort_scatter_k<IPT, true, true><<<nb, SBS, 0, s>>>(idx, nullptr, nullptr, n, len, shift, ntiles, tab, kb, vb, present, guard_flag());
-    else sort_scatter_k<IPT, true, false><<<nb, SBS, 0, s>>>(idx, nullptr, nullptr, n, len, shift, ntiles, tab, kb, vb, present, guard_flag());
+    if (self) sort_scatter_k<IPT, true, OFFS_SCAN_COUNTS><<<nb, SBS, 0, s>>>(idx, nullptr, nullptr, n, len, shift, ntiles, tab, kb, vb, present, gd);
+    else sort_scatter_k<IPT, true, OFFS_TABLE><<<nb, SBS, 0, s>>>(idx, nullptr, nullptr, n, len, shift, ntiles, tab, kb, vb, present, gd);
   } else {
-    if (self) sort_scatter_k<IPT, false, true><<<nb, SBS, 0, s>>>(nullptr, ka, va, n, len, shift, ntiles, tab, kb, vb, nullptr, guard_flag());
-    else sort_scatter_k<IPT, false, false><<<nb, SBS, 0, s>>>(nullptr, ka, va, n, len, shift, ntiles, tab, kb, vb, nullptr, guard_flag());
+    if (self) sort_scatter_k<IPT, false, OFFS_SCAN_COUNTS><<<nb, SBS, 0, s>>>(nullptr, ka, va, n, len, shift, ntiles, tab, kb, vb, nullptr, gd);
+    else sort_scatter_k<IPT, false, OFFS_TABLE><<<nb, SBS, 0, s>>>(nullptr, ka, va, n, len, shift, ntiles, tab, kb, vb, nullptr, gd);
   }
 }
 
@@ -649,9 +676,9 @@ int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inn
   for (int ps = 0; ps < passes; ++ps) {
     int* kb = bufk[ps & 1];
     int* vb = bufv[ps & 1];
-    if (ipt == 2) sort_pass<2>(s, ps, passes, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
-    else if (ipt == 8) sort_pass<8>(s, ps, passes, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
-    else sort_pass<32>(s, ps, passes, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
+    if (ipt == 2) sort_pass<2>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
+    else if (ipt == 8) sort_pass<8>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
+    else sort_pass<32>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
     ka = kb;
     va = vb;
   }

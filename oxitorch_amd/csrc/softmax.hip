@@ -200,7 +200,8 @@ __global__ __launch_bounds__(BS) void sm_bwd_col_k(const float* __restrict__ y, 
 // Cross-entropy.
 
 constexpr int CE_BS = 256;
-constexpr int CE_U = 4;  // float4 loads in flight per thread per step
+constexpr int CE_U = 4;   // forward: float4 loads in flight per thread per step
+constexpr int CE_BU = 1;  // backward: float4s per thread (one per thread streams fastest)
 
 // One block per row. lse[row] = max + log(sum exp(x - max));
 // picked[row] = (x[t] - max) - log(sum)  (the reference's ls[row, t]).
@@ -282,16 +283,16 @@ __global__ __launch_bounds__(CE_BS) void ce_bwd_k(const float* __restrict__ logi
     const f4* p = reinterpret_cast<const f4*>(xr);
     f4* q = reinterpret_cast<f4*>(dr);
     const int c4 = C >> 2;
-    const int per_block = CE_BS * CE_U;
+    const int per_block = CE_BS * CE_BU;
     const int c0 = blockIdx.x * per_block + threadIdx.x;
-    f4 v[CE_U];
+    f4 v[CE_BU];
 #pragma unroll
-    for (int u = 0; u < CE_U; ++u) {
+    for (int u = 0; u < CE_BU; ++u) {
       const int c = c0 + u * CE_BS;
       if (c < c4) v[u] = ld_stream(p + c);
     }
 #pragma unroll
-    for (int u = 0; u < CE_U; ++u) {
+    for (int u = 0; u < CE_BU; ++u) {
       const int c = c0 + u * CE_BS;
       if (c < c4) {
         f4 e = exp4(v[u] - l);
@@ -307,9 +308,9 @@ __global__ __launch_bounds__(CE_BS) void ce_bwd_k(const float* __restrict__ logi
       }
     }
   } else {
-    const int per_block = CE_BS * CE_U;
+    const int per_block = CE_BS * CE_BU;
     const int c0 = blockIdx.x * per_block + threadIdx.x;
-    for (int u = 0; u < CE_U; ++u) {
+    for (int u = 0; u < CE_BU; ++u) {
       const int c = c0 + u * CE_BS;
       if (c < C) {
         float e = expf(xr[c] - l);
@@ -476,7 +477,7 @@ int oxi_cross_entropy_bwd(const float* logits, const int64_t* targets, const flo
   OXI_CHECK_INIT();
   const int vec = (c % 4 == 0 && aligned16({logits, dlogits})) ? 1 : 0;
   const int64_t units = vec ? c / 4 : c;
-  const unsigned gx = (unsigned)ceil_div(units, CE_BS * CE_U);
+  const unsigned gx = (unsigned)ceil_div(units, CE_BS * CE_BU);
   const bool nts = nt_stores(n * c * 4);
   if (n > 65535) {
     // grid.y is limited; launch row slabs
