@@ -40,7 +40,7 @@ def assert_close(got, want, rtol=RTOL, atol=ATOL, what=""):
     assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
     err = np.abs(got - want)
     tol = atol + rtol * np.abs(want)
-    bad = ~(err <= tol)
+    bad = ~(err <= tol) & ~(np.isnan(got) & np.isnan(want))  # NaN must meet NaN
     if bad.any():
         i = np.flatnonzero(bad.ravel())[0]
         raise AssertionError(
