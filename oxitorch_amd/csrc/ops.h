@@ -66,6 +66,9 @@ constexpr float GELU_K = 0.044715f;
 constexpr float GELU_C = 0.7978845608028654f;  // float(np.sqrt(2/np.pi))
 constexpr float SQRT1_2 = 0.7071067811865476f;
 constexpr float INV_SQRT_2PI = 0.3989422804014327f;
+constexpr float LOG2E_F = 1.44269502f;        // log2(e) rounded to f32
+constexpr float LOG2E_LO = 1.925963033e-8f;   // log2(e) - LOG2E_F
+constexpr float LN2_F = 0.693147181f;
 
 // y = (x*0.5) * (tanh(((x + (x*(x*x))*K) * C)) + 1)
 struct GeluTanhFwd {
@@ -111,19 +114,63 @@ struct GeluTanhBwd {
   }
 };
 
-// Exact GELU: y = (0.5*x) * (1 + erf(x/sqrt2)).
-struct GeluErfFwd {
-  __device__ __forceinline__ float operator()(float x) const {
-    return (0.5f * x) * (1.0f + erff(x * SQRT1_2));
-  }
+// Standard normal CDF Phi(x) and density phi(x) for the exact GELU, through
+// erfc(z) = exp(-z*z) * t * Q(t) with z = |x|/sqrt2 and t = 1/(1 + z/2).
+// Q is a degree-10 polynomial in t fitted in float64 (weighted least
+// squares, relative error) to erfcx(z)/t over t in (0, 1]: 1.1e-8 relative
+// before rounding; Q(0) = 1/(2*sqrt(pi)). One exp per element and no branch:
+// ROCm's erff evaluates two polynomial ranges and GELU inputs straddle its
+// branch point in every wave, which made the forward ALU-bound.
+// exp(-x*x/2) carries the rounding error of x*x (fma residual), and |x| is
+// clamped at 20 there (exp(-200) is 0 in f32) so that +-inf stay finite.
+// In float32 this Phi stays within 6.5e-7 relative of float64, and
+// x * Phi(x) within 4e-7 absolute; evaluating Phi as 1 - E/2 for x >= 0 and
+// E/2 for x < 0 avoids the cancellation of 0.5 * (1 + erf(x/sqrt2)).
+struct NormalCdfPdf {
+  float cdf, pdf;
 };
 
-// dy/dx = 0.5*(1 + erf(x/sqrt2)) + x * exp(-x*x/2) / sqrt(2*pi)
+__device__ __forceinline__ NormalCdfPdf normal_cdf_pdf(float x) {
+  const float ax = fabsf(x);
+  const float z = ax * SQRT1_2;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float q = 0.042352393f;
+  q = fmaf(q, t, -0.23085676f);
+  q = fmaf(q, t, 0.48617718f);
+  q = fmaf(q, t, -0.4469757f);
+  q = fmaf(q, t, 0.1270884f);
+  q = fmaf(q, t, -0.057232074f);
+  q = fmaf(q, t, 0.093000494f);
+  q = fmaf(q, t, 0.17537685f);
+  q = fmaf(q, t, 0.24688059f);
+  q = fmaf(q, t, 0.28209385f);
+  q = fmaf(q, t, 0.2820948f);
+  // exp(-x*x/2) = 2^a * (1 + d): a = p*L rounded, p = -(x*x)/2 rounded; d
+  // carries, to first order, the product's rounding (fma residual), the part
+  // of log2(e) below L, and the rounding of x*x. 2^a is v_exp_f32.
+  const float xe = fminf(ax, 20.0f);
+  const float hh = xe * xe;
+  const float hl = fmaf(xe, xe, -hh);  // x*x = hh + hl exactly
+  const float p = -0.5f * hh;
+  const float a = p * LOG2E_F;
+  const float r = fmaf(p, LOG2E_LO, fmaf(p, LOG2E_F, -a));
+  const float d = fmaf(r, LN2_F, -0.5f * hl);
+  const float e0 = __builtin_amdgcn_exp2f(a);
+  const float e = fmaf(e0, d, e0);
+  const float half = 0.5f * ((t * q) * e);  // erfc(|x|/sqrt2) / 2
+  return {x < 0.0f ? half : 1.0f - half, e * INV_SQRT_2PI};
+}
+
+// Exact GELU: y = x * Phi(x)  (= 0.5*x*(1 + erf(x/sqrt2))).
+struct GeluErfFwd {
+  __device__ __forceinline__ float operator()(float x) const { return x * normal_cdf_pdf(x).cdf; }
+};
+
+// dy/dx = Phi(x) + x * phi(x)
 struct GeluErfBwd {
   __device__ __forceinline__ float operator()(float x, float g) const {
-    const float cdf = 0.5f * (1.0f + erff(x * SQRT1_2));
-    const float pdf = expf(-0.5f * (x * x)) * INV_SQRT_2PI;
-    return g * (cdf + x * pdf);
+    const NormalCdfPdf p = normal_cdf_pdf(x);
+    return g * (p.cdf + x * p.pdf);
   }
 };
 
