@@ -31,12 +31,13 @@ __device__ __forceinline__ float rsum(float v, float* lds) { return group_sum<TP
 // Forward, register-resident rows.
 
 template <int TPR, int NV, bool LN, bool NTS>
-__global__ __launch_bounds__(BS) void norm_fwd_k(const float* __restrict__ x, const float* __restrict__ w,
+__global__ __launch_bounds__((row_block_threads(TPR))) void norm_fwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  const float* __restrict__ b, float* __restrict__ y,
                                                  float* __restrict__ mean, float* __restrict__ rstd,
                                                  int64_t rows, int H, float eps) {
-  constexpr int GPB = BS / TPR;
-  __shared__ float lds[BS / 64];
+  constexpr int NT = row_block_threads(TPR);
+  constexpr int GPB = NT / TPR;
+  __shared__ float lds[NT / 64];
   const int t = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * GPB + threadIdx.x / TPR;
   if (row >= rows) return;  // GPB == 1 whenever TPR > 64: the whole block leaves together
@@ -355,8 +356,11 @@ bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
   return true;
 }
 
-// Picks (TPR, NV) for a vectorized row of h4 float4s; 0 when it does not fit.
-int pick_cfg(int64_t h4) {
+// (TPR, NV) of the backward for a vectorized row of h4 float4s; 0 when it
+// does not fit. The backward keeps its rows multi-float4 per lane: it walks
+// rows grid-strided with column partials, and one-wave groups let 16 rows
+// share a block.
+int pick_bwd_cfg(int64_t h4) {
   if (h4 <= 64) return 641;
   if (h4 <= 128) return 642;
   if (h4 <= 192) return 643;
@@ -372,7 +376,8 @@ void launch_fwd_cfg(int cfg, hipStream_t s, const float* x, const float* w, cons
                     float* rstd, int64_t rows, int h, float eps) {
 #define OXI_FWD(TPR, NV)                                                                                   \
   case TPR * 10 + NV:                                                                                      \
-    norm_fwd_k<TPR, NV, LN, NTS><<<dim3((unsigned)ceil_div(rows, BS / TPR)), dim3(BS), 0, s>>>(x, w, b, y, \
+    norm_fwd_k<TPR, NV, LN, NTS><<<dim3((unsigned)ceil_div(rows, row_block_threads(TPR) / TPR)),          \
+                                   dim3(row_block_threads(TPR)), 0, s>>>(x, w, b, y,                         \
                                                                                              mean, rstd,   \
                                                                                              rows, h, eps); \
     break;
@@ -394,7 +399,7 @@ template <bool LN>
 int launch_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
                int64_t rows, int64_t H, float eps) {
   hipStream_t s = stream();
-  const int cfg = vec_ok(H, {x, w, b, y}) ? pick_cfg(H / 4) : 0;
+  const int cfg = vec_ok(H, {x, w, b, y}) ? pick_row_cfg(H / 4) : 0;
   const int h = (int)H;
   if (nt_stores(rows * H * 4)) launch_fwd_cfg<LN, true>(cfg, s, x, w, b, y, mean, rstd, rows, h, eps);
   else launch_fwd_cfg<LN, false>(cfg, s, x, w, b, y, mean, rstd, rows, h, eps);
@@ -428,13 +433,14 @@ int launch_bwd(const float* x, const float* w, const float* mean, const float* r
                float* dx, float* dw, float* db, int64_t rows, int64_t H) {
   hipStream_t s = stream();
   const bool need_part = dw || (LN && db);
-  const int cfg = vec_ok(H, {x, w, g, dx}) ? pick_cfg(H / 4) : 0;
+  const int cfg = vec_ok(H, {x, w, g, dx}) ? pick_bwd_cfg(H / 4) : 0;
   const int tpr = cfg ? cfg / 10 : BS;
   const int nt = tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : BS;  // bwd_threads<TPR, NV>()
   const int gpb = nt / tpr;
   // Blocks: enough to fill the chip, few enough that the partial rows stay
   // a small fraction of the row traffic.
   int64_t nblk = ceil_div(rows, gpb);
+  // (measured: 2 blocks per CU beat 3 and 4 for 4096-float rows)
   const int64_t cap = (int64_t)cu_count() * (nt == 1024 ? 1 : 2);
   if (need_part && nblk > cap) nblk = cap;
   if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;

@@ -45,6 +45,26 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
 // lose 16-35% on 0.5-1 GB outputs and ~10% on 12 MB ones.
 inline bool nt_stores(int64_t bytes) { return bytes < ((int64_t)32 << 20) || bytes > ((int64_t)320 << 20); }
 
+// Threads per block of a row kernel whose rows take TPR threads: 256 (several
+// rows per block) when TPR divides 256, else one row per block of TPR.
+constexpr int row_block_threads(int tpr) { return (256 % tpr == 0) ? 256 : tpr; }
+
+// (TPR, NV) for rows of h4 float4s, encoded TPR*10 + NV; 0 when the row does
+// not fit in registers. Rows keep several float4s per lane: measured on
+// MI355X, one float4 per lane (192 threads per 768-float row, 1024 per
+// 4096-float row) made the layer-norm forward 30% slower, the block-wide
+// reductions over many waves costing more than the access pattern gains.
+inline int pick_row_cfg(int64_t h4) {
+  if (h4 <= 64) return 641;
+  if (h4 <= 128) return 642;
+  if (h4 <= 192) return 643;
+  if (h4 <= 256) return 644;
+  if (h4 <= 512) return 2562;
+  if (h4 <= 1024) return 2564;
+  if (h4 <= 2048) return 2568;
+  return 0;
+}
+
 template <int TPR, int NV>
 struct RowTile {
   f4 v[NV];

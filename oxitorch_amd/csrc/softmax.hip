@@ -67,9 +67,11 @@ __device__ __forceinline__ void group_online(Online& o, float* lds) {
 // Last-dim kernels, register-resident rows.
 
 template <int TPR, int NV, bool LOG, bool NTS>
-__global__ __launch_bounds__(BS) void sm_fwd_k(const float* __restrict__ x, float* __restrict__ y, int64_t rows, int H) {
-  constexpr int GPB = BS / TPR;
-  __shared__ float lds[2 * (BS / 64)];
+__global__ __launch_bounds__((row_block_threads(TPR))) void sm_fwd_k(const float* __restrict__ x, float* __restrict__ y,
+                                                                  int64_t rows, int H) {
+  constexpr int NT = row_block_threads(TPR);
+  constexpr int GPB = NT / TPR;
+  __shared__ float lds[2 * (NT / 64)];
   const int t = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * GPB + threadIdx.x / TPR;
   if (row >= rows) return;
@@ -91,7 +93,7 @@ __global__ __launch_bounds__(BS) void sm_fwd_k(const float* __restrict__ x, floa
       xt.v[k] = LOG ? z : e;
     }
   }
-  s = group_sum<TPR, float>(s, lds + BS / 64);
+  s = group_sum<TPR, float>(s, lds + NT / 64);
   if constexpr (LOG) {
     const float L = logf(s);
 #pragma unroll
@@ -104,10 +106,11 @@ __global__ __launch_bounds__(BS) void sm_fwd_k(const float* __restrict__ x, floa
 }
 
 template <int TPR, int NV, bool LOG, bool NTS>
-__global__ __launch_bounds__(BS) void sm_bwd_k(const float* __restrict__ y, const float* __restrict__ g,
-                                               float* __restrict__ dx, int64_t rows, int H) {
-  constexpr int GPB = BS / TPR;
-  __shared__ float lds[BS / 64];
+__global__ __launch_bounds__((row_block_threads(TPR))) void sm_bwd_k(const float* __restrict__ y, const float* __restrict__ g,
+                                                                  float* __restrict__ dx, int64_t rows, int H) {
+  constexpr int NT = row_block_threads(TPR);
+  constexpr int GPB = NT / TPR;
+  __shared__ float lds[NT / 64];
   const int t = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * GPB + threadIdx.x / TPR;
   if (row >= rows) return;
@@ -324,16 +327,6 @@ __global__ __launch_bounds__(CE_BS) void ce_bwd_k(const float* __restrict__ logi
 // ---------------------------------------------------------------------------
 // Host dispatch.
 
-int pick_cfg(int64_t h4) {
-  if (h4 <= 64) return 641;
-  if (h4 <= 128) return 642;
-  if (h4 <= 192) return 643;
-  if (h4 <= 256) return 644;
-  if (h4 <= 512) return 2562;
-  if (h4 <= 1024) return 2564;
-  if (h4 <= 2048) return 2568;
-  return 0;
-}
 
 bool aligned16(std::initializer_list<const void*> ps) {
   for (const void* p : ps)
@@ -356,13 +349,15 @@ template <bool LOG>
 int launch_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inner) {
   hipStream_t s = stream();
   if (inner == 1) {
-    const int cfg = (len % 4 == 0 && aligned16({x, y})) ? pick_cfg(len / 4) : 0;
+    const int cfg = (len % 4 == 0 && aligned16({x, y})) ? pick_row_cfg(len / 4) : 0;
     const int h = (int)len;
     const bool nts = nt_stores(outer * len * 4);
 #define OXI_SMF(TPR, NV)                                                                                            \
   case TPR * 10 + NV:                                                                                               \
-    if (nts) sm_fwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(x, y, outer, h);  \
-    else sm_fwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(x, y, outer, h);     \
+    if (nts) sm_fwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),         \
+                                           dim3(row_block_threads(TPR)), 0, s>>>(x, y, outer, h);                    \
+    else sm_fwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),            \
+                                         dim3(row_block_threads(TPR)), 0, s>>>(x, y, outer, h);                      \
     break;
     switch (cfg) {
       OXI_SMF(64, 1)
@@ -372,7 +367,7 @@ int launch_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inn
       OXI_SMF(256, 2)
       OXI_SMF(256, 4)
       OXI_SMF(256, 8)
-      default:
+                default:
         sm_fwd_loop_k<LOG><<<dim3((unsigned)outer), dim3(BS), 0, s>>>(x, y, outer, h);
     }
 #undef OXI_SMF
@@ -386,13 +381,15 @@ template <bool LOG>
 int launch_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t len, int64_t inner) {
   hipStream_t s = stream();
   if (inner == 1) {
-    const int cfg = (len % 4 == 0 && aligned16({y, g, dx})) ? pick_cfg(len / 4) : 0;
+    const int cfg = (len % 4 == 0 && aligned16({y, g, dx})) ? pick_row_cfg(len / 4) : 0;
     const int h = (int)len;
     const bool nts = nt_stores(outer * len * 4);
 #define OXI_SMB(TPR, NV)                                                                                        \
   case TPR * 10 + NV:                                                                                           \
-    if (nts) sm_bwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(y, g, dx, outer, h);  \
-    else sm_bwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, BS / TPR)), dim3(BS), 0, s>>>(y, g, dx, outer, h);     \
+    if (nts) sm_bwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),         \
+                                           dim3(row_block_threads(TPR)), 0, s>>>(y, g, dx, outer, h);                \
+    else sm_bwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),            \
+                                         dim3(row_block_threads(TPR)), 0, s>>>(y, g, dx, outer, h);                  \
     break;
     switch (cfg) {
       OXI_SMB(64, 1)
@@ -402,7 +399,7 @@ int launch_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t
       OXI_SMB(256, 2)
       OXI_SMB(256, 4)
       OXI_SMB(256, 8)
-      default:
+                default:
         sm_bwd_loop_k<LOG><<<dim3((unsigned)outer), dim3(BS), 0, s>>>(y, g, dx, outer, h);
     }
 #undef OXI_SMB
