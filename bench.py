@@ -5,7 +5,9 @@ A "step" is one forward+backward pass of a BASELINE.json config over one batch
 of synthetic, seeded input that is already resident in HBM, driven through the
 liboxihip C-ABI (include/oxihip.h) in the order the host core launches it.
 Default workload: config 2, F.layer_norm(affine) -> exact-erf gelu, fwd+bwd,
-fp32, x (16384, 4096). `--config c1|c3|c4|c5` selects the other configs.
+fp32, x (16384, 4096). `--config c1|c3|c4|c5` selects the other configs;
+`--config f4` times one AdamW step over GPT-2 small's 148 parameter tensors
+(the optimizer step after backward).
 
 value = algorithmic bytes per step / wall time per step (GB/s). Algorithmic
 bytes are the per-op minimum (each op reads its inputs once and writes its
@@ -40,9 +42,12 @@ METRIC = "achieved HBM GB/s (% of MI355X peak) + rows/s, norm/softmax/embed fwd+
 
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled
 # by the same counters' reading of a 1 GiB copy (FETCH x2.0, WRITE x1.0);
-# the runs and the per-kernel table are in profiles/pmc_traffic_c2.md.
+# the runs and the per-kernel tables are in profiles/pmc_traffic_c2.md and
+# profiles/pmc_traffic_f4.md.
 TRAFFIC_BYTES = {
     "c2": {"layer_norm_fwd": 538.2e6, "gelu_erf_fwd": 537.0e6, "gelu_erf_bwd": 805.5e6, "layer_norm_bwd": 840.2e6},
+    # profiles/pmc_traffic_f4.md: the 5 launches of one multi-parameter call
+    "f4": {"adamw_step_multi": 3484.9e6},
 }
 
 
@@ -55,7 +60,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-oracle baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-copy-probe", action="store_true")
@@ -306,7 +311,76 @@ class C5(Workload):
         ref.index_select_bwd(de.reshape(-1, self.H), h["W"].shape, 0, ids)
 
 
-WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5}
+def gpt2_small_param_shapes(V=50257, T=1024, H=768, L=12):
+    """Parameter shapes of GPT-2 small with tied embeddings: 148 tensors,
+    124,439,808 floats."""
+    block = [(H,), (H,), (H, 3 * H), (3 * H,), (H, H), (H,), (H,), (H,), (H, 4 * H), (4 * H,), (4 * H, H), (H,)]
+    return [(V, H), (T, H)] + block * L + [(H,), (H,)]
+
+
+class F4(Workload):
+    """One AdamW step (decoupled decay) over every parameter of GPT-2 small,
+    one tensor per parameter as a model holds them, through the multi-slice
+    entry point the host core calls; new values ping-pong between two
+    buffers per parameter."""
+
+    cpu_full = True
+
+    def __init__(self, hip):
+        super().__init__(hip)
+        self.shapes = gpt2_small_param_shapes()
+        sizes = [int(np.prod(s)) for s in self.shapes]
+        self.sizes = sizes
+        N = sum(sizes)
+        self.rows = N
+        self.name = f"F4 AdamW step, GPT-2 small parameters ({len(sizes)} tensors, {N:,} fp32)"
+        r = np.random.default_rng(44)
+        flat = {k: r.standard_normal(N, dtype=np.float32) for k in ("p", "g")}
+        flat["m"] = r.standard_normal(N, dtype=np.float32) * np.float32(0.01)
+        flat["v"] = r.random(N, dtype=np.float32) * np.float32(1e-4)
+        self.host = flat
+        A = hip.DeviceArray
+        self.dev = []
+        off = 0
+        for n in sizes:
+            d = {k: self.D(flat[k][off:off + n]) for k in ("p", "g", "m", "v")}
+            d["q"] = A((n,))
+            self.dev.append(d)
+            off += n
+        self.hyper = (6e-4, 0.9, 0.95, 1e-8, 0.1, 1)
+        t = 10
+        fwd = [(d["p"].ptr, d["g"].ptr, d["m"].ptr, d["v"].ptr, d["q"].ptr, n, t) for d, n in zip(self.dev, sizes)]
+        back = [(d["q"].ptr, d["g"].ptr, d["m"].ptr, d["v"].ptr, d["p"].ptr, n, t) for d, n in zip(self.dev, sizes)]
+        self.tables = [hip.slice_array(hip.AdamWSlice, fwd), hip.slice_array(hip.AdamWSlice, back)]
+        self.flip = 0
+        self.bytes_per_step = 28 * N  # read p, g, m, v; write p', m, v
+
+    def _multi(self):
+        L, c = self.hip.lib, self.hip.check
+        c(L.oxi_adamw_step_multi(self.tables[self.flip], len(self.sizes), *self.hyper))
+        self.flip ^= 1
+
+    def kernels(self):
+        return [("adamw_step_multi", self._multi, self.bytes_per_step)]
+
+    def per_tensor(self):
+        """The same step with one oxi_adamw_step launch per parameter."""
+        L, c = self.hip.lib, self.hip.check
+        lr, b1, b2, eps, wd, dec = self.hyper
+
+        def run():
+            for d, n in zip(self.dev, self.sizes):
+                c(L.oxi_adamw_step(d["p"].ptr, d["g"].ptr, d["m"].ptr, d["v"].ptr, d["q"].ptr, n, lr, b1, b2, eps, wd,
+                                   dec, 10))
+        return [("adamw_step_per_tensor", run, self.bytes_per_step)]
+
+    def cpu_step(self, ref, lo, hi):
+        h = self.host
+        m, v = h["m"][lo:hi].copy(), h["v"][lo:hi].copy()
+        ref.adamw_step(h["p"][lo:hi], h["g"][lo:hi], m, v, 10, *self.hyper)
+
+
+WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f4": F4}
 
 
 # ---------------------------------------------------------------------------
@@ -362,8 +436,10 @@ def copy_probe(hip, nbytes=1 << 30):
 def cpu_baseline(wl, budget_s):
     from oracle import ref  # the checker/baseline, never the measured product
 
-    if isinstance(wl, (C4, C5)):
-        # a dense dW per call makes row samples unrepresentative: time the full workload once
+    if isinstance(wl, (C4, C5)) or getattr(wl, "cpu_full", False):
+        # a dense dW per call makes row samples unrepresentative (C4, C5), and
+        # per-call overhead would swamp small element ranges (F4): time the
+        # full workload once
         t0 = time.perf_counter()
         wl.cpu_step(ref, 0, wl.rows)
         done = wl.rows
@@ -444,6 +520,11 @@ def main():
                      "algorithmic_bytes": d["bytes"]},
         "cpu_baseline": None,
     }
+    if hasattr(wl, "per_tensor"):
+        alt = wl.per_tensor()
+        ms_alt = time_steps(hip, alt, max(3, min(args.steps, 10)))
+        line["per_tensor_launches"] = {"ms_per_step": round(ms_alt, 5),
+                                       "gbs": round(wl.bytes_per_step / (ms_alt * 1e-3) / 1e9, 2)}
     if not args.no_copy_probe:
         log("copy probe")
         line["stream_copy_gbs"] = copy_probe(hip)

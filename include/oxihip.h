@@ -244,6 +244,64 @@ int oxi_embedding_bwd(const float* g, const int64_t* ids, int64_t n,
 int oxi_reduce(int kind, const float* x, const int64_t* x_strides,
                const int64_t* shape, int ndim, int dim, float* out);
 
+/* ------------------------------------------------------------------------ */
+/* Optimizer steps over one flat parameter (n contiguous floats).            */
+
+/* SGD for one parameter: with momentum > 0, buf = momentum*buf + g (buf is
+ * updated in place, n floats, zero before the first step) and the update is
+ * buf, or g + momentum*buf when `nesterov`; without momentum the update is g
+ * and `buf` may be NULL. p_out = p - lr*update; `p_out` may equal `p`.
+ * Elementwise f32 in the reference's operation order, so bit-exact with it.
+ * Replaces Sgd::step_param (crates/oxi-autograd/src/optim.rs:104-137); the
+ * nesterov-without-momentum check of RustSgd::new
+ * (crates/oxi-bindings/src/lib.rs:842-846) is repeated here. */
+int oxi_sgd_step(const float* p, const float* g, float* buf, float* p_out,
+                 int64_t n, float lr, float momentum, int nesterov);
+/* Adam / AdamW for one parameter at step t >= 1 (the parameter's own step
+ * counter after increment): bias corrections 1 - beta^t in f32 powf; classic
+ * Adam (decoupled = 0) adds weight_decay*p to the gradient, AdamW
+ * (decoupled = 1) subtracts lr*weight_decay*p after the adaptive step. The
+ * moments m, v (n floats each, zero before step 1) are updated in place;
+ * `p_out` may equal `p`. Bit-exact with the reference's f32 loop. Replaces
+ * AdamW::step_param (crates/oxi-autograd/src/optim.rs:223-262). */
+int oxi_adamw_step(const float* p, const float* g, float* m, float* v, float* p_out,
+                   int64_t n, float lr, float beta1, float beta2, float eps,
+                   float weight_decay, int decoupled, int64_t t);
+
+/* One parameter of a multi-parameter step: its operands as for the
+ * single-parameter entry points. Slices must not overlap one another
+ * (`p_out` may equal the slice's own `p`). */
+typedef struct oxi_sgd_slice {
+  const float* p;
+  const float* g;
+  float* buf; /* NULL allowed when momentum == 0 */
+  float* p_out;
+  int64_t n;
+} oxi_sgd_slice;
+
+typedef struct oxi_adamw_slice {
+  const float* p;
+  const float* g;
+  float* m;
+  float* v;
+  float* p_out;
+  int64_t n;
+  int64_t t; /* this parameter's step count, >= 1 */
+} oxi_adamw_slice;
+
+/* One optimizer step over a whole parameter list, each slice updated exactly
+ * as by oxi_sgd_step / oxi_adamw_step (bit-identical), in few launches: up to
+ * 32 slices per launch, their descriptors passed as kernel arguments, so the
+ * many small parameters of a model (biases, norm weights) cost no launch of
+ * their own. All arguments are checked before anything is launched.
+ * Replaces Sgd::step / AdamW::step (crates/oxi-autograd/src/optim.rs:143-148,
+ * 267-272) as driven by step_all (crates/oxi-bindings/src/lib.rs:815-826). */
+int oxi_sgd_step_multi(const oxi_sgd_slice* slices, int count,
+                       float lr, float momentum, int nesterov);
+int oxi_adamw_step_multi(const oxi_adamw_slice* slices, int count,
+                         float lr, float beta1, float beta2, float eps,
+                         float weight_decay, int decoupled);
+
 #ifdef __cplusplus
 }
 #endif

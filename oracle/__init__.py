@@ -272,6 +272,29 @@ class ref:
         return y
 
 
+    @staticmethod
+    def sgd_step(p, g, buf, lr, momentum=0.0, nesterov=False):
+        """One Sgd step; `buf` (momentum state, updated in place) may be None
+        when momentum == 0. Returns the new parameter values."""
+        p, g = _f32(p), _f32(g)
+        out = np.empty_like(p)
+        bp = _fp(buf) if buf is not None else None
+        lib().ref_sgd_step(_fp(p), _fp(g), bp, _fp(out), ctypes.c_int64(p.size), ctypes.c_float(lr),
+                           ctypes.c_float(momentum), ctypes.c_int(int(nesterov)))
+        return out
+
+    @staticmethod
+    def adamw_step(p, g, m, v, t, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=1e-2, decoupled=True):
+        """One AdamW/Adam step at per-parameter step t (m, v updated in place).
+        Returns the new parameter values."""
+        p, g = _f32(p), _f32(g)
+        out = np.empty_like(p)
+        lib().ref_adamw_step(_fp(p), _fp(g), _fp(m), _fp(v), _fp(out), ctypes.c_int64(p.size), ctypes.c_float(lr),
+                             ctypes.c_float(beta1), ctypes.c_float(beta2), ctypes.c_float(eps),
+                             ctypes.c_float(weight_decay), ctypes.c_int(int(decoupled)), ctypes.c_int64(t))
+        return out
+
+
 from . import closed_form  # noqa: E402  (float64 arbiter)
 
 __all__ = ["ref", "closed_form", "build", "lib"]

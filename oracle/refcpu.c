@@ -513,3 +513,42 @@ EXPORT void ref_gelu_erf_bwd(const float* x, const float* g, float* dx, int64_t 
     dx[i] = g[i] * (cdf + v * pdf);
   }
 }
+
+/* ---- optimizer steps (crates/oxi-autograd/src/optim.rs) ------------------ */
+
+/* Sgd::step_param (optim.rs:104-137) for one parameter with a gradient:
+ * buf = momentum*buf + g (buf starts at zeros, optim.rs:113-115);
+ * update = nesterov ? g + momentum*buf : buf, or g without momentum;
+ * p_out = p - lr*update. `buf` may be NULL when momentum == 0. */
+EXPORT void ref_sgd_step(const float* p, const float* g, float* buf, float* p_out, int64_t n, float lr, float momentum,
+                         int nesterov) {
+  for (int64_t i = 0; i < n; ++i) {
+    float upd = g[i];
+    if (momentum > 0.0f) {
+      buf[i] = momentum * buf[i] + g[i];
+      upd = nesterov ? g[i] + momentum * buf[i] : buf[i];
+    }
+    p_out[i] = p[i] - lr * upd;
+  }
+}
+
+/* AdamW::step_param (optim.rs:223-262) for one parameter with a gradient at
+ * step t: bc1 = 1 - beta1^t, bc2 = 1 - beta2^t in f32 powf (optim.rs:233-234);
+ * classic Adam (decoupled = 0) folds weight_decay*p into the gradient, AdamW
+ * subtracts lr*weight_decay*p after the adaptive step. */
+EXPORT void ref_adamw_step(const float* p, const float* g, float* m, float* v, float* p_out, int64_t n, float lr,
+                           float beta1, float beta2, float eps, float weight_decay, int decoupled, int64_t t) {
+  const float bc1 = 1.0f - powf(beta1, (float)t);
+  const float bc2 = 1.0f - powf(beta2, (float)t);
+  for (int64_t i = 0; i < n; ++i) {
+    const float val = p[i];
+    const float ge = (!decoupled && weight_decay != 0.0f) ? g[i] + weight_decay * val : g[i];
+    m[i] = beta1 * m[i] + (1.0f - beta1) * ge;
+    v[i] = beta2 * v[i] + (1.0f - beta2) * ge * ge;
+    const float mh = m[i] / bc1;
+    const float vh = v[i] / bc2;
+    float next = val - lr * mh / (sqrtf(vh) + eps);
+    if (decoupled && weight_decay != 0.0f) next -= lr * weight_decay * val;
+    p_out[i] = next;
+  }
+}

@@ -25,7 +25,7 @@ from oxitorch_amd._native import (  # noqa: F401
     version,
     zeros,
 )
-from oxitorch_amd import nn  # noqa: E402
+from oxitorch_amd import nn, optim  # noqa: E402
 
 __all__ = [
     "Tensor",
@@ -40,6 +40,7 @@ __all__ = [
     "memory_stats",
     "nn",
     "no_grad",
+    "optim",
     "set_default_device",
     "set_grad_enabled",
     "synchronize",

@@ -88,6 +88,10 @@ _SIGS = {
     "oxi_embedding_fwd": [vp, vp, c_i64, c_i64, c_i64, vp],
     "oxi_embedding_bwd": [vp, vp, c_i64, c_i64, c_i64, vp],
     "oxi_reduce": [c_int, vp, P_i64, P_i64, c_int, c_int, vp],
+    "oxi_sgd_step": [vp, vp, vp, vp, c_i64, c_float, c_float, c_int],
+    "oxi_adamw_step": [vp, vp, vp, vp, vp, c_i64, c_float, c_float, c_float, c_float, c_float, c_int, c_i64],
+    "oxi_sgd_step_multi": [vp, c_int, c_float, c_float, c_int],
+    "oxi_adamw_step_multi": [vp, c_int, c_float, c_float, c_float, c_float, c_float, c_int],
 }
 
 for _name, _args in _SIGS.items():
@@ -366,6 +370,43 @@ def reduce(kind: str, x: DeviceArray, dim: int, x_strides=None, shape=None) -> D
     call("oxi_reduce", REDUCE.index(kind), x.ptr, _i64arr(x_strides or row_major_strides(shape)), _i64arr(shape),
          len(shape), dim, out.ptr)
     return out
+
+
+def sgd_step(p: DeviceArray, g: DeviceArray, buf: DeviceArray | None, lr, momentum=0.0, nesterov=False,
+             out: DeviceArray | None = None) -> DeviceArray:
+    """One SGD step over a flat parameter; `buf` is updated in place. `out`
+    defaults to a new array; pass `p` to update in place."""
+    out = out if out is not None else DeviceArray(p.shape)
+    call("oxi_sgd_step", p.ptr, g.ptr, buf.ptr if buf is not None else None, out.ptr, p.size, lr, momentum,
+         int(bool(nesterov)))
+    return out
+
+
+def adamw_step(p: DeviceArray, g: DeviceArray, m: DeviceArray, v: DeviceArray, t: int, lr, beta1=0.9, beta2=0.999,
+               eps=1e-8, weight_decay=1e-2, decoupled=True, out: DeviceArray | None = None) -> DeviceArray:
+    """One Adam/AdamW step at step count `t`; `m`, `v` are updated in place."""
+    out = out if out is not None else DeviceArray(p.shape)
+    call("oxi_adamw_step", p.ptr, g.ptr, m.ptr, v.ptr, out.ptr, p.size, lr, beta1, beta2, eps, weight_decay,
+         int(bool(decoupled)), t)
+    return out
+
+
+class SgdSlice(ctypes.Structure):
+    """oxi_sgd_slice"""
+    _fields_ = [("p", vp), ("g", vp), ("buf", vp), ("p_out", vp), ("n", c_i64)]
+
+
+class AdamWSlice(ctypes.Structure):
+    """oxi_adamw_slice"""
+    _fields_ = [("p", vp), ("g", vp), ("m", vp), ("v", vp), ("p_out", vp), ("n", c_i64), ("t", c_i64)]
+
+
+def slice_array(cls, rows):
+    """A ctypes array of `cls` built from tuples of field values."""
+    arr = (cls * max(1, len(rows)))()
+    for i, r in enumerate(rows):
+        arr[i] = cls(*r)
+    return arr
 
 
 class Timer:

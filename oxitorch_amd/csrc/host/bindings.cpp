@@ -6,6 +6,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <algorithm>
 #include <cmath>
 #include <sstream>
 
@@ -170,6 +171,33 @@ py::array_t<float> to_numpy(const PyTensor& self) {
   py::array_t<float> a(shape);
   if (!v.empty()) std::memcpy(a.mutable_data(), v.data(), v.size() * sizeof(float));
   return a;
+}
+
+PyTensor& tensor_item(const py::handle& item) {
+  if (!py::isinstance<PyTensor>(item)) throw py::type_error("optimizer parameters must be oxitorch.Tensor objects");
+  return item.cast<PyTensor&>();
+}
+
+// step_all (bindings lib.rs:815-826): the optimizer advances each Var in
+// list order and rebinds the caller's Tensor objects, which keep their
+// identity; those before a failing parameter stay advanced. A Tensor listed
+// twice is refused before any step, as the reference's exclusive borrow of
+// each list element refuses it.
+template <class F>
+void step_all(const py::list& params, F&& step) {
+  std::vector<Var*> vars;
+  vars.reserve(params.size());
+  for (const py::handle& item : params) {
+    Var* v = &tensor_item(item).v;
+    if (std::find(vars.begin(), vars.end(), v) != vars.end())
+      throw std::runtime_error("Already borrowed: the same Tensor appears twice in the parameter list");
+    vars.push_back(v);
+  }
+  step(vars);
+}
+
+void zero_grads(const py::list& params) {  // RustSgd::zero_grad (bindings lib.rs:864-872)
+  for (const py::handle& item : params) tensor_item(item).v.zero_grad();
 }
 
 }  // namespace
@@ -495,4 +523,37 @@ PYBIND11_MODULE(_native, m) {
   m.def("embedding", [](const std::vector<int64_t>& indices, const PyTensor& w) {
     return PyTensor(aops::embedding(indices, w.v));
   });
+
+  // Elementwise clamp on the device (binary max then min against scalar
+  // constants), for gradient-value clipping; detached.
+  m.def("clamp", [](const PyTensor& x, float lo, float hi) {
+    const Tensor& t = x.value();
+    Tensor a = t_binary_op("max", t, t_scalar_full(t.shape, lo, t.dev()));
+    return leaf(t_binary_op("min", a, t_scalar_full(t.shape, hi, t.dev())));
+  });
+
+  // ---- optimizers (bindings lib.rs:807-936): state lives in the host core,
+  // each step rebinds the given Tensor objects to their updated leaves.
+  py::class_<Sgd>(m, "RustSgd")
+      .def(py::init([](double lr, double momentum, bool nesterov) {
+             if (nesterov && momentum <= 0.0) throw py::value_error("nesterov momentum requires momentum > 0");
+             return Sgd((float)lr, (float)momentum, nesterov);
+           }),
+           py::arg("lr") = 0.01, py::arg("momentum") = 0.0, py::arg("nesterov") = false)
+      .def_property(
+          "lr", [](const Sgd& o) { return (double)o.lr(); }, [](Sgd& o, double lr) { o.set_lr((float)lr); })
+      .def_static("zero_grad", &zero_grads)
+      .def("step", [](Sgd& o, const py::list& params) { step_all(params, [&](std::vector<Var*>& v) { o.step(v); }); });
+  py::class_<AdamW>(m, "RustAdamW")
+      .def(py::init([](double lr, std::pair<double, double> betas, double eps, double weight_decay, bool decoupled) {
+             return AdamW((float)lr, (float)betas.first, (float)betas.second, (float)eps, (float)weight_decay,
+                          decoupled);
+           }),
+           py::arg("lr") = 1e-3, py::arg("betas") = std::make_pair(0.9, 0.999), py::arg("eps") = 1e-8,
+           py::arg("weight_decay") = 1e-2, py::arg("decoupled") = true)
+      .def_property(
+          "lr", [](const AdamW& o) { return (double)o.lr(); }, [](AdamW& o, double lr) { o.set_lr((float)lr); })
+      .def_static("zero_grad", &zero_grads)
+      .def("step",
+           [](AdamW& o, const py::list& params) { step_all(params, [&](std::vector<Var*>& v) { o.step(v); }); });
 }

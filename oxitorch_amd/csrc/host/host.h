@@ -218,4 +218,40 @@ Var cross_entropy(const Var& logits, const std::vector<int64_t>& targets);
 Var embedding(const std::vector<int64_t>& indices, const Var& weight);
 }  // namespace aops
 
+// ---- optimizers (crates/oxi-autograd/src/optim.rs) ------------------------------
+// All state (velocities, moments, per-parameter step counters) lives here as
+// device tensors, indexed by parameter position and allocated lazily on the
+// first step that parameter has a gradient. Each step rebinds the parameter to
+// a fresh requires_grad leaf holding the updated values (optim.rs:24-28).
+
+class Sgd {
+ public:
+  Sgd(float lr, float momentum, bool nesterov) : lr_(lr), momentum_(momentum), nesterov_(nesterov) {}
+  float lr() const { return lr_; }
+  void set_lr(float lr) { lr_ = lr; }
+  void step_param(size_t index, Var& param);
+  void step(std::vector<Var*>& params);
+
+ private:
+  float lr_, momentum_;
+  bool nesterov_;
+  std::vector<std::optional<Tensor>> velocities_;
+};
+
+class AdamW {
+ public:
+  AdamW(float lr, float beta1, float beta2, float eps, float weight_decay, bool decoupled)
+      : lr_(lr), beta1_(beta1), beta2_(beta2), eps_(eps), wd_(weight_decay), decoupled_(decoupled) {}
+  float lr() const { return lr_; }
+  void set_lr(float lr) { lr_ = lr; }
+  void step_param(size_t index, Var& param);
+  void step(std::vector<Var*>& params);
+
+ private:
+  float lr_, beta1_, beta2_, eps_, wd_;
+  bool decoupled_;
+  std::vector<std::optional<Tensor>> moments_, sq_moments_;
+  std::vector<uint64_t> steps_;
+};
+
 }  // namespace oxt

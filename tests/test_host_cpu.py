@@ -196,3 +196,131 @@ def test_backward_error_paths(ox):
     t = cpu(ox, np.ones(3))
     with pytest.raises(ValueError, match="does not require grad"):
         t.backward()
+
+
+# ---- optimizers: argument checks and schedules (no device work) ----------------------
+
+def test_optimizer_argument_errors():
+    from oxitorch_amd import capi
+
+    with pytest.raises(ValueError, match="nesterov momentum requires momentum > 0"):
+        capi.call("oxi_sgd_step", None, None, None, None, 4, 0.1, 0.0, 1)
+    with pytest.raises(ValueError, match="negative size"):
+        capi.call("oxi_sgd_step", None, None, None, None, -1, 0.1, 0.0, 0)
+    with pytest.raises(ValueError, match="step count must be >= 1"):
+        capi.call("oxi_adamw_step", None, None, None, None, None, 4, 0.1, 0.9, 0.999, 1e-8, 0.0, 1, 0)
+    with pytest.raises(ValueError, match="NULL tensor pointer"):
+        capi.call("oxi_adamw_step", None, None, None, None, None, 4, 0.1, 0.9, 0.999, 1e-8, 0.0, 1, 1)
+    # empty parameters are a no-op before any device use
+    capi.call("oxi_adamw_step", None, None, None, None, None, 0, 0.1, 0.9, 0.999, 1e-8, 0.0, 1, 1)
+    capi.call("oxi_sgd_step", None, None, None, None, 0, 0.1, 0.9, 1)
+
+
+def test_native_optimizer_construction(ox):
+    """RustSgd / RustAdamW constructors and lr property
+    (crates/oxi-bindings/src/lib.rs:838-893)."""
+    from oxitorch_amd import _native
+    import oxitorch_amd.optim as op
+
+    with pytest.raises(ValueError, match="nesterov momentum requires momentum > 0"):
+        _native.RustSgd(0.1, 0.0, True)
+    with pytest.raises(ValueError, match="nesterov momentum requires momentum > 0"):
+        op.Sgd([], lr=0.1, nesterov=True)
+    s = _native.RustSgd()
+    assert s.lr == pytest.approx(0.01)
+    s.lr = 0.25
+    assert s.lr == 0.25
+    a = _native.RustAdamW()
+    assert a.lr == pytest.approx(1e-3)
+    opt = op.AdamW([], lr=0.5)
+    assert opt.lr == 0.5 and opt.weight_decay == 1e-2 and opt.betas == (0.9, 0.999)
+    assert op.Adam([]).weight_decay == 0.0
+    opt.step()  # an empty parameter list steps nothing
+    with pytest.raises(TypeError, match="oxitorch.Tensor"):
+        _native.RustAdamW().step([1.0])
+
+
+def test_optimizer_refuses_host_tensors(ox):
+    """Parameters staged on the host are not stepped on the CPU."""
+    import oxitorch_amd.optim as op
+
+    w = ox.from_numpy(np.ones(3, np.float32), True, device="cpu")
+    w.grad = ox.from_numpy(np.ones(3, np.float32), device="cpu")
+    with pytest.raises(NotImplementedError, match="on a host"):
+        op.Sgd([w], lr=0.1).step()
+
+
+class _FakeOpt:
+    def __init__(self, lr):
+        self.lr = lr
+
+
+def test_step_lr_schedule():
+    """python/tests/test_phase4_training.py:110-120."""
+    import oxitorch_amd.optim as op
+
+    o = _FakeOpt(1.0)
+    s = op.StepLR(o, step_size=2, gamma=0.5)
+    lrs = []
+    for _ in range(6):
+        lrs.append(o.lr)
+        s.step()
+    assert lrs == pytest.approx([1.0, 1.0, 0.5, 0.5, 0.25, 0.25])
+    assert s.get_last_lr() == [o.lr]
+
+
+def test_cosine_and_lambda_schedules():
+    """python/tests/test_phase4_training.py:123-143."""
+    import math
+
+    import oxitorch_amd.optim as op
+
+    o = _FakeOpt(1.0)
+    s = op.CosineAnnealingLR(o, T_max=4, eta_min=0.0)
+    lrs = []
+    for _ in range(5):
+        lrs.append(o.lr)
+        s.step()
+    assert lrs[0] == pytest.approx(1.0)
+    assert lrs[1] == pytest.approx((1 + math.cos(math.pi / 4)) / 2)
+    assert lrs[2] == pytest.approx(0.5)
+    assert lrs[4] == pytest.approx(0.0, abs=1e-6)
+    o = _FakeOpt(0.1)
+    s = op.LambdaLR(o, lr_lambda=lambda t: 0.5**t)
+    lrs = []
+    for _ in range(3):
+        lrs.append(o.lr)
+        s.step()
+    assert lrs == pytest.approx([0.1, 0.05, 0.025])
+
+
+def test_warmup_then_cosine_sequential():
+    """python/tests/test_phase4_training.py:146-176."""
+    import oxitorch_amd.optim as op
+
+    o = _FakeOpt(0.1)
+    warm = op.LinearWarmup(o, warmup_epochs=2)
+    cosine = op.CosineAnnealingLR(o, T_max=6)
+    seq = op.SequentialLR(o, [warm, cosine], milestones=[2])
+    lrs = []
+    for _ in range(9):
+        lrs.append(round(float(o.lr), 6))
+        seq.step()
+    assert lrs[0] == pytest.approx(0.05)
+    assert lrs[1] == pytest.approx(0.1)
+    assert lrs[2] == pytest.approx(0.1)
+    assert lrs[4] == pytest.approx(0.075)
+    assert lrs[6] == pytest.approx(0.025)
+    assert lrs[8] == pytest.approx(0.0, abs=1e-6)
+    o = _FakeOpt(0.2)
+    warm = op.LinearWarmup(o, warmup_epochs=2)
+    cosine = op.CosineAnnealingLR(o, T_max=10, eta_min=0.0)
+    seq = op.SequentialLR(o, [warm, cosine], milestones=[2])
+    assert cosine.base_lr == pytest.approx(0.2)
+    seq.step()
+    seq.step()
+    assert o.lr == pytest.approx(0.2)
+    with pytest.raises(ValueError, match="milestones"):
+        op.SequentialLR(o, [warm, cosine], milestones=[])
+    with pytest.raises(ValueError):
+        op.LinearWarmup(o, warmup_epochs=-1)

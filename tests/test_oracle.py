@@ -355,3 +355,101 @@ def test_planted_mistakes_are_caught():
     xs = r.standard_normal((2, 5))
     gs = r.standard_normal((2, 5))
     assert not fd_check(cf.softmax, xs, softmax_bwd_missing_dot(xs, gs), gs)
+
+
+# ---------------------------------------------------------------------------
+# Optimizer steps (crates/oxi-autograd/src/optim.rs)
+
+def _adam_f64(p, g, m, v, t, lr, b1, b2, eps, wd, decoupled):
+    p, g = p.astype(np.float64), g.astype(np.float64)
+    ge = g + wd * p if (not decoupled and wd != 0) else g
+    m = b1 * m + (1 - b1) * ge
+    v = b2 * v + (1 - b2) * ge * ge
+    nxt = p - lr * (m / (1 - b1 ** t)) / (np.sqrt(v / (1 - b2 ** t)) + eps)
+    if decoupled and wd != 0:
+        nxt = nxt - lr * wd * p
+    return nxt, m, v
+
+
+def test_kat_sgd_momentum_and_nesterov():
+    """crates/oxi-autograd/src/optim.rs:314-334: three momentum steps of a
+    constant gradient 0.5 (lr 0.1, momentum 0.9), and one Nesterov step."""
+    buf = np.zeros(1, np.float32)
+    val = np.ones(1, np.float32)
+    for want in (1.0 - 0.05, 0.95 - 0.095, 0.855 - 0.1355):
+        val = ref.sgd_step(val, np.array([0.5], np.float32), buf, 0.1, 0.9)
+        assert abs(float(val[0]) - want) < 1e-6
+    buf = np.zeros(1, np.float32)
+    val = ref.sgd_step(np.ones(1, np.float32), np.array([0.5], np.float32), buf, 0.1, 0.9, nesterov=True)
+    assert abs(float(val[0]) - (1.0 - 0.1 * 0.95)) < 1e-6
+    # no momentum: plain descent, no state
+    val = ref.sgd_step(np.ones(1, np.float32), np.array([0.5], np.float32), None, 0.1, 0.0)
+    assert abs(float(val[0]) - 0.95) < 1e-7
+
+
+def test_kat_adamw_and_classic_adam():
+    """optim.rs:366-404: two AdamW steps against the float64 closed form, and
+    classic Adam folding the decay into the gradient."""
+    m, v = np.zeros(1, np.float32), np.zeros(1, np.float32)
+    val = np.ones(1, np.float32)
+    vf, mf, vvf = np.ones(1), np.zeros(1), np.zeros(1)
+    for t in (1, 2):
+        val = ref.adamw_step(val, np.array([0.5], np.float32), m, v, t, 0.1, 0.9, 0.999, 1e-8, 0.1, True)
+        vf, mf, vvf = _adam_f64(vf, np.array([0.5]), mf, vvf, t, 0.1, 0.9, 0.999, 1e-8, 0.1, True)
+        assert abs(float(val[0]) - float(vf[0])) < 1e-5
+    m, v = np.zeros(1, np.float32), np.zeros(1, np.float32)
+    got = ref.adamw_step(np.ones(1, np.float32), np.array([0.5], np.float32), m, v, 1, 0.1, 0.9, 0.999, 1e-8, 0.1,
+                         False)
+    ge = 0.5 + 0.1 * 1.0
+    want = 1.0 - 0.1 * ((0.1 * ge) / 0.1) / (np.sqrt((0.001 * ge * ge) / 0.001) + 1e-8)
+    assert abs(float(got[0]) - want) < 1e-5
+
+
+@pytest.mark.parametrize("decoupled", [True, False])
+def test_adam_matches_float64_over_steps(decoupled):
+    """Random parameters, 5 steps with fresh gradients: the f32 oracle stays
+    within 1e-6 relative of the float64 closed form; a planted mistake (bias
+    correction dropped from the second moment) does not."""
+    r = rng(31)
+    p = r.standard_normal(257).astype(np.float32)
+    m, v = np.zeros_like(p), np.zeros_like(p)
+    pf, mf, vf = p.astype(np.float64), np.zeros(p.size), np.zeros(p.size)
+    for t in range(1, 6):
+        g = r.standard_normal(p.size).astype(np.float32)
+        p = ref.adamw_step(p, g, m, v, t, 1e-2, 0.9, 0.999, 1e-8, 0.05, decoupled)
+        pf, mf, vf = _adam_f64(pf, g, mf, vf, t, 1e-2, 0.9, 0.999, 1e-8, 0.05, decoupled)
+        assert np.allclose(p, pf, rtol=1e-6, atol=1e-7)
+    # planted mistake, carried through the same recurrence: v not bias-corrected
+    r = rng(31)
+    q = r.standard_normal(257).astype(np.float64)
+    mq, vq = np.zeros(q.size), np.zeros(q.size)
+    for t in range(1, 6):
+        g = r.standard_normal(q.size).astype(np.float32).astype(np.float64)
+        ge = g + 0.05 * q if not decoupled else g
+        mq = 0.9 * mq + 0.1 * ge
+        vq = 0.999 * vq + 0.001 * ge * ge
+        q = q - 1e-2 * (mq / (1 - 0.9 ** t)) / (np.sqrt(vq) + 1e-8) - (1e-2 * 0.05 * q if decoupled else 0)
+    assert not np.allclose(p, q, rtol=1e-6, atol=1e-7)
+
+
+def test_sgd_matches_float64_over_steps():
+    r = rng(32)
+    p = r.standard_normal(300).astype(np.float32)
+    buf = np.zeros_like(p)
+    pf, bf = p.astype(np.float64), np.zeros(p.size)
+    for _ in range(4):
+        g = r.standard_normal(p.size).astype(np.float32)
+        p = ref.sgd_step(p, g, buf, 0.05, 0.9, nesterov=True)
+        bf = 0.9 * bf + g
+        pf = pf - 0.05 * (g + 0.9 * bf)
+        assert np.allclose(p, pf, rtol=1e-6, atol=1e-6)
+    # planted mistake, carried through the same recurrence: the Nesterov
+    # update without its gradient term
+    r = rng(32)
+    q = r.standard_normal(300).astype(np.float64)
+    bq = np.zeros(q.size)
+    for _ in range(4):
+        g = r.standard_normal(q.size).astype(np.float32).astype(np.float64)
+        bq = 0.9 * bq + g
+        q = q - 0.05 * (0.9 * bq)
+    assert not np.allclose(p, q, rtol=1e-6, atol=1e-6)
