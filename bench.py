@@ -6,8 +6,9 @@ of synthetic, seeded input that is already resident in HBM, driven through the
 liboxihip C-ABI (include/oxihip.h) in the order the host core launches it.
 Default workload: config 2, F.layer_norm(affine) -> exact-erf gelu, fwd+bwd,
 fp32, x (16384, 4096). `--config c1|c3|c4|c5` selects the other configs;
-`--config f4` times one AdamW step over GPT-2 small's 148 parameter tensors
-(the optimizer step after backward).
+`--config f3` times masked_select and the row scatter (fwd+bwd), and
+`--config f4` one AdamW step over GPT-2 small's 148 parameter tensors (the
+optimizer step after backward).
 
 value = algorithmic bytes per step / wall time per step (GB/s). Algorithmic
 bytes are the per-op minimum (each op reads its inputs once and writes its
@@ -42,10 +43,13 @@ METRIC = "achieved HBM GB/s (% of MI355X peak) + rows/s, norm/softmax/embed fwd+
 
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled
 # by the same counters' reading of a 1 GiB copy (FETCH x2.0, WRITE x1.0);
-# the runs and the per-kernel tables are in profiles/pmc_traffic_c2.md and
-# profiles/pmc_traffic_f4.md.
+# the runs and the per-kernel tables are in profiles/pmc_traffic_c2.md,
+# profiles/pmc_traffic_f3.md and profiles/pmc_traffic_f4.md.
 TRAFFIC_BYTES = {
     "c2": {"layer_norm_fwd": 538.2e6, "gelu_erf_fwd": 537.0e6, "gelu_erf_bwd": 805.5e6, "layer_norm_bwd": 840.2e6},
+    # profiles/pmc_traffic_f3.md: all launches of each C-ABI call
+    "f3": {"masked_select_fwd": 970.8e6, "masked_select_bwd": 425.7e6, "scatter_rows_fwd": 311.2e6,
+           "scatter_rows_bwd": 407.3e6},
     # profiles/pmc_traffic_f4.md: the 5 launches of one multi-parameter call
     "f4": {"adamw_step_multi": 3484.9e6},
 }
@@ -380,7 +384,81 @@ class F4(Workload):
         ref.adamw_step(h["p"][lo:hi], h["g"][lo:hi], m, v, 10, *self.hyper)
 
 
-WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f4": F4}
+class F3(Workload):
+    """The remaining indexing ops, fwd+bwd: masked_select over x (16384, 4096)
+    with a density-0.5 mask of the same shape, and the last-write-wins row
+    scatter of 16384 rows (with repeats) into a (50257, 768) table."""
+
+    cpu_full = True
+
+    def __init__(self, hip):
+        super().__init__(hip)
+        R, H = 16384, 4096
+        V, D, n = 50257, 768, 16384
+        self.R, self.H, self.V, self.Dm, self.n = R, H, V, D, n
+        self.name = "F3 masked_select (16384,4096) p=0.5 + scatter_dim0 16384 rows into (50257,768), fwd+bwd fp32"
+        r = np.random.default_rng(33)
+        x = r.standard_normal((R, H), dtype=np.float32)
+        m = (r.random((R, H), dtype=np.float32) < 0.5).astype(np.float32)
+        base = r.standard_normal((V, D), dtype=np.float32)
+        ids = r.integers(0, V, n).astype(np.int64)
+        vals = r.standard_normal((n, D), dtype=np.float32)
+        gs = r.standard_normal((V, D), dtype=np.float32)
+        self.count = int((m != 0).sum())
+        gm = r.standard_normal(self.count, dtype=np.float32)
+        self.host = dict(x=x, m=m, base=base, ids=ids, vals=vals, gs=gs, gm=gm)
+        for k, v in self.host.items():
+            setattr(self, "d_" + k, self.D(v))
+        A = hip.DeviceArray
+        self.gx = A((R, H))
+        self.out_s, self.gb, self.gv = A((V, D)), A((V, D)), A((n, D))
+        self.rows = R + n
+        E = R * H
+        # masked_select moves x and the mask in, the picks and its record (one
+        # bit per element) out; its VJP reads the record and the upstream
+        # gradient and writes grad_x
+        self.op_bytes = dict(masked_select_fwd=8 * E + 4 * self.count + E // 8,
+                             masked_select_bwd=E // 8 + 4 * self.count + 4 * E,
+                             scatter_rows_fwd=8 * V * D + 8 * n, scatter_rows_bwd=8 * V * D + 4 * n * D + 8 * n)
+        self.bytes_per_step = sum(self.op_bytes.values())
+        st = hip._i64arr
+        self.s_x, self.s_shape = st((H, 1)), st((R, H))
+        self.picked = None
+        self.record = hip.masked_select_record((R, H))
+
+    def _msel(self):
+        L, c = self.hip.lib, self.hip.check
+        out, cnt = self.hip.vp(), self.hip.c_i64(0)
+        c(L.oxi_masked_select(self.d_x.ptr, self.s_x, self.d_m.ptr, self.s_x, self.s_shape, 2,
+                              self.hip.ctypes.byref(out), self.hip.ctypes.byref(cnt), self.record.ptr))
+        if self.picked:
+            c(L.oxi_hip_free(self.picked))
+        self.picked = out.value
+
+    def kernels(self):
+        L, c = self.hip.lib, self.hip.check
+        V, D, n, b = self.V, self.Dm, self.n, self.op_bytes
+        return [
+            ("masked_select_fwd", self._msel, b["masked_select_fwd"]),
+            ("masked_select_bwd", lambda: c(L.oxi_masked_select_bwd(
+                self.record.ptr, self.s_shape, 2, self.d_gm.ptr, self.count, self.gx.ptr, self.s_x,
+                self.R * self.H)), b["masked_select_bwd"]),
+            ("scatter_rows_fwd", lambda: c(L.oxi_scatter_rows(self.d_base.ptr, V, D, self.d_ids.ptr, n,
+                                                              self.d_vals.ptr, self.out_s.ptr)),
+             b["scatter_rows_fwd"]),
+            ("scatter_rows_bwd", lambda: c(L.oxi_scatter_rows_bwd(self.d_gs.ptr, V, D, self.d_ids.ptr, n,
+                                                                  self.gb.ptr, self.gv.ptr)), b["scatter_rows_bwd"]),
+        ]
+
+    def cpu_step(self, ref, lo, hi):
+        h = self.host
+        ref.masked_select(h["x"], h["m"])
+        ref.masked_select_bwd(h["x"].shape, h["m"], h["gm"])
+        ref.scatter_dim0(h["base"], h["ids"], h["vals"])
+        ref.scatter_dim0_bwd(h["gs"], h["ids"], h["vals"].shape)
+
+
+WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f3": F3, "f4": F4}
 
 
 # ---------------------------------------------------------------------------

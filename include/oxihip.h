@@ -231,6 +231,52 @@ int oxi_embedding_fwd(const float* W, const int64_t* ids, int64_t n,
 int oxi_embedding_bwd(const float* g, const int64_t* ids, int64_t n,
                       int64_t V, int64_t D, float* dW);
 
+/* Row scatter, last write wins: out (rows, inner) = base with row idx[p]
+ * replaced by values row p, for p in order, so a row written twice keeps the
+ * later values. `idx` (n int64 on device) may hold negatives in [-rows, rows),
+ * which wrap; ids are validated on the host, the kernels only guard. base,
+ * values and out are contiguous; out must not alias them. Replaces
+ * Tensor::scatter_dim0 (crates/oxi-tensor/src/lib.rs:895-932). */
+int oxi_scatter_rows(const float* base, int64_t rows, int64_t inner,
+                     const int64_t* idx, int64_t n, const float* values, float* out);
+/* VJP of the row scatter for upstream g (rows, inner): gbase = g * 0 on every
+ * written row and g * 1 elsewhere (a multiply, as the reference's mask);
+ * gvalues (n, inner) row p = g row idx[p] when p is that row's last writer,
+ * zeros otherwise. Either output may be NULL. Replaces the VJP of
+ * aops::scatter_dim0 (crates/oxi-autograd/src/ops.rs:531-600). */
+int oxi_scatter_rows_bwd(const float* g, int64_t rows, int64_t inner,
+                         const int64_t* idx, int64_t n, float* gbase, float* gvalues);
+/* Boolean-mask selection over the broadcast of x and mask (strides
+ * broadcast-expanded to `shape`): the x values at grid points whose mask value
+ * is not zero, in row-major order of `shape`. As in the reference, which marks
+ * unpicked points NaN and drops every NaN, a picked NaN of x is dropped too.
+ * The output size depends on the data: the call waits for the device to count
+ * the picks, then allocates `*out` (`*count` floats, NULL when none) with
+ * oxi_hip_alloc; the caller frees it with oxi_hip_free. When `record` is not
+ * NULL (device memory of oxi_masked_select_record_bytes bytes, 8-byte
+ * aligned) it receives the selection's record, one bit per grid point plus
+ * per-tile offsets, which oxi_masked_select_bwd reads in place of x and the
+ * mask. Replaces Tensor::masked_select (crates/oxi-tensor/src/lib.rs:939-961). */
+int oxi_masked_select(const float* x, const int64_t* x_strides,
+                      const float* mask, const int64_t* m_strides,
+                      const int64_t* shape, int ndim, float** out, int64_t* count,
+                      void* record);
+/* Bytes of the record of a selection over `shape` (host-side, no device work). */
+int oxi_masked_select_record_bytes(const int64_t* shape, int ndim, int64_t* bytes);
+/* VJP of oxi_masked_select from its record: grad_x (x_numel floats,
+ * row-major of x's own shape) = zeros plus, for each picked grid point in
+ * grid order, the next upstream gradient g[k] added at the point's x element,
+ * so points that broadcast onto one element accumulate in grid order.
+ * `gx_strides` are the row-major strides of x's own shape expanded to `shape`,
+ * 0 on the dims where x is broadcast; they are checked against x_numel.
+ * `count` is the forward's pick count; a record whose count differs raises
+ * the device guard flag (oxi_hip_sync reports it) and no gradient beyond
+ * `count` is read. Replaces the VJP of aops::masked_select
+ * (crates/oxi-autograd/src/ops.rs:609-667), which walks the mask again. */
+int oxi_masked_select_bwd(const void* record, const int64_t* shape, int ndim,
+                          const float* g, int64_t count,
+                          float* grad_x, const int64_t* gx_strides, int64_t x_numel);
+
 /* ------------------------------------------------------------------------ */
 /* Dim reductions.                                                           */
 

@@ -273,6 +273,77 @@ class ref:
 
 
     @staticmethod
+    def scatter_dim0(base, idx, values):
+        """Tensor::scatter_dim0: rows idx[p] of `base` replaced by values[p]
+        in order (last write wins)."""
+        base, values = _f32(base), _f32(values)
+        idx = np.ascontiguousarray(idx, dtype=np.int64)
+        rows = base.shape[0]
+        inner = int(np.prod(base.shape[1:], dtype=np.int64))
+        out = np.empty_like(base)
+        rc = lib().ref_scatter_dim0(_fp(base), ctypes.c_int64(rows), ctypes.c_int64(inner), _ip(idx),
+                                    ctypes.c_int64(len(idx)), _fp(values), _fp(out))
+        if rc:
+            raise IndexError("index out of range")
+        return out
+
+    @staticmethod
+    def scatter_dim0_bwd(g, idx, n_values_shape):
+        """(gbase, gvalues) of scatter_dim0 for upstream g (base's shape)."""
+        g = _f32(g)
+        idx = np.ascontiguousarray(idx, dtype=np.int64)
+        rows = g.shape[0]
+        inner = int(np.prod(g.shape[1:], dtype=np.int64))
+        gb = np.empty_like(g)
+        gv = np.empty(n_values_shape, np.float32)
+        lib().ref_scatter_dim0_bwd(_fp(g), ctypes.c_int64(rows), ctypes.c_int64(inner), _ip(idx),
+                                   ctypes.c_int64(len(idx)), _fp(gb), _fp(gv))
+        return gb, gv
+
+    @staticmethod
+    def _bcast_elem_strides(a, shape):
+        v = np.broadcast_to(a, shape)
+        return np.ascontiguousarray([s // 4 for s in v.strides], dtype=np.int64)
+
+    @staticmethod
+    def _rm_bcast_strides(own_shape, shape):
+        """Row-major strides of `own_shape`, expanded to `shape` with 0 on
+        broadcast (size-1 or missing) dims (aops::masked_select's flat strides)."""
+        rm = [1] * len(own_shape)
+        for d in range(len(own_shape) - 2, -1, -1):
+            rm[d] = rm[d + 1] * own_shape[d + 1]
+        off = len(shape) - len(own_shape)
+        out = [0 if d < off or own_shape[d - off] == 1 else rm[d - off] for d in range(len(shape))]
+        return np.ascontiguousarray(out, dtype=np.int64)
+
+    @staticmethod
+    def masked_select(x, mask):
+        """Tensor::masked_select over the broadcast of x and mask."""
+        x, mask = _f32(x), _f32(mask)
+        shape = np.broadcast_shapes(x.shape, mask.shape)
+        n = int(np.prod(shape, dtype=np.int64))
+        out = np.empty(max(n, 1), np.float32)
+        lib().ref_masked_select.restype = ctypes.c_int64
+        cnt = lib().ref_masked_select(_fp(x), _ip(ref._bcast_elem_strides(x, shape)), _fp(mask),
+                                      _ip(ref._bcast_elem_strides(mask, shape)),
+                                      _ip(np.ascontiguousarray(shape, dtype=np.int64)), ctypes.c_int(len(shape)),
+                                      _fp(out))
+        return out[:cnt].copy()
+
+    @staticmethod
+    def masked_select_bwd(x_shape, mask, g):
+        """Gradient of x for masked_select(x, mask) with upstream g."""
+        mask, g = _f32(mask), _f32(g)
+        x_shape = tuple(x_shape)
+        shape = np.broadcast_shapes(x_shape, mask.shape)
+        gx = np.empty(x_shape, np.float32)
+        lib().ref_masked_select_bwd(_fp(mask), _ip(ref._rm_bcast_strides(mask.shape, shape)),
+                                    _ip(np.ascontiguousarray(shape, dtype=np.int64)), ctypes.c_int(len(shape)),
+                                    _fp(g), _fp(gx), _ip(ref._rm_bcast_strides(x_shape, shape)),
+                                    ctypes.c_int64(gx.size))
+        return gx
+
+    @staticmethod
     def sgd_step(p, g, buf, lr, momentum=0.0, nesterov=False):
         """One Sgd step; `buf` (momentum state, updated in place) may be None
         when momentum == 0. Returns the new parameter values."""

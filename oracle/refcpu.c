@@ -552,3 +552,100 @@ EXPORT void ref_adamw_step(const float* p, const float* g, float* m, float* v, f
     p_out[i] = next;
   }
 }
+
+/* ---- scatter_dim0 (Tensor::scatter_dim0, crates/oxi-tensor/src/lib.rs:895-932) */
+
+/* out = base (rows, inner) with row idx[p] replaced by values[p] for p in
+ * order (last write wins). Returns 0, or 1 when an index is out of range
+ * (checked before anything is written, lib.rs:912-919). */
+EXPORT int ref_scatter_dim0(const float* base, int64_t rows, int64_t inner, const int64_t* idx, int64_t n,
+                            const float* values, float* out) {
+  for (int64_t p = 0; p < n; ++p) {
+    const int64_t r = idx[p] < 0 ? rows + idx[p] : idx[p];
+    if (r < 0 || r >= rows) return 1;
+  }
+  memcpy(out, base, sizeof(float) * (size_t)(rows * inner));
+  for (int64_t p = 0; p < n; ++p) {
+    const int64_t r = idx[p] < 0 ? rows + idx[p] : idx[p];
+    memcpy(out + r * inner, values + p * inner, sizeof(float) * (size_t)inner);
+  }
+  return 0;
+}
+
+/* VJP of aops::scatter_dim0 (crates/oxi-autograd/src/ops.rs:531-600):
+ * gbase = g * mask with mask 0 on every written row and 1 elsewhere
+ * (a multiply, so a negative g gives -0 on written rows); slot p of gvalues
+ * gets g's row idx[p] when p is that row's last writer, zeros otherwise.
+ * Either output may be NULL. */
+EXPORT void ref_scatter_dim0_bwd(const float* g, int64_t rows, int64_t inner, const int64_t* idx, int64_t n,
+                                 float* gbase, float* gvalues) {
+  int64_t* last = (int64_t*)malloc(sizeof(int64_t) * (size_t)(rows > 0 ? rows : 1));
+  for (int64_t r = 0; r < rows; ++r) last[r] = -1;
+  for (int64_t p = 0; p < n; ++p) last[idx[p] < 0 ? rows + idx[p] : idx[p]] = p;
+  if (gbase)
+    for (int64_t r = 0; r < rows; ++r) {
+      const float m = last[r] >= 0 ? 0.0f : 1.0f;
+      for (int64_t i = 0; i < inner; ++i) gbase[r * inner + i] = g[r * inner + i] * m;
+    }
+  if (gvalues)
+    for (int64_t p = 0; p < n; ++p) {
+      const int64_t r = idx[p] < 0 ? rows + idx[p] : idx[p];
+      for (int64_t i = 0; i < inner; ++i) gvalues[p * inner + i] = last[r] == p ? g[r * inner + i] : 0.0f;
+    }
+  free(last);
+}
+
+/* ---- masked_select (Tensor::masked_select, lib.rs:939-961) ------------------ */
+
+/* Row-major walk of the broadcast `shape` (iterate::map_n): an element is
+ * picked when its mask value != 0; the reference marks unpicked elements NaN
+ * and then drops every NaN, so a picked NaN of x is dropped too. Writes the
+ * picks to `out` (capacity: the grid size) and returns their count. */
+EXPORT int64_t ref_masked_select(const float* x, const int64_t* xs, const float* m, const int64_t* ms,
+                                 const int64_t* shape, int ndim, float* out) {
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) n *= shape[d];
+  int64_t idx[16] = {0};
+  int64_t cnt = 0;
+  for (int64_t e = 0; e < n; ++e) {
+    int64_t ox = 0, om = 0;
+    for (int d = 0; d < ndim; ++d) {
+      ox += idx[d] * xs[d];
+      om += idx[d] * ms[d];
+    }
+    const float v = m[om] == 0.0f ? NAN : x[ox];
+    if (!isnan(v)) out[cnt++] = v;
+    for (int d = ndim - 1; d >= 0; --d) {
+      if (++idx[d] < shape[d]) break;
+      idx[d] = 0;
+    }
+  }
+  return cnt;
+}
+
+/* VJP of aops::masked_select (crates/oxi-autograd/src/ops.rs:609-667): walk
+ * the same grid; each point whose mask value != 0 takes the next upstream
+ * gradient and adds it to x's element at gx_strides (row-major strides of x's
+ * own shape, 0 on broadcast dims), starting from zeros. The picks are counted
+ * from the mask alone (ops.rs:650-653). Mask strides: row-major of the mask's
+ * own shape, 0 on broadcast dims (ops.rs:628-640). */
+EXPORT void ref_masked_select_bwd(const float* m, const int64_t* ms, const int64_t* shape, int ndim, const float* g,
+                                  float* gx, const int64_t* gx_strides, int64_t x_numel) {
+  for (int64_t i = 0; i < x_numel; ++i) gx[i] = 0.0f;
+  int64_t n = 1;
+  for (int d = 0; d < ndim; ++d) n *= shape[d];
+  int64_t idx[16] = {0};
+  int64_t pick = 0;
+  for (int64_t e = 0; e < n; ++e) {
+    int64_t om = 0, ox = 0;
+    for (int d = 0; d < ndim; ++d) {
+      om += idx[d] * ms[d];
+      ox += idx[d] * gx_strides[d];
+    }
+    if (m[om] != 0.0f) gx[ox] += g[pick++];
+    for (int d = ndim - 1; d >= 0; --d) {
+      if (++idx[d] < shape[d]) break;
+      idx[d] = 0;
+    }
+  }
+}

@@ -88,6 +88,11 @@ _SIGS = {
     "oxi_embedding_fwd": [vp, vp, c_i64, c_i64, c_i64, vp],
     "oxi_embedding_bwd": [vp, vp, c_i64, c_i64, c_i64, vp],
     "oxi_reduce": [c_int, vp, P_i64, P_i64, c_int, c_int, vp],
+    "oxi_scatter_rows": [vp, c_i64, c_i64, vp, c_i64, vp, vp],
+    "oxi_scatter_rows_bwd": [vp, c_i64, c_i64, vp, c_i64, vp, vp],
+    "oxi_masked_select": [vp, P_i64, vp, P_i64, P_i64, c_int, ctypes.POINTER(vp), ctypes.POINTER(c_i64), vp],
+    "oxi_masked_select_record_bytes": [P_i64, c_int, ctypes.POINTER(c_i64)],
+    "oxi_masked_select_bwd": [vp, P_i64, c_int, vp, c_i64, vp, P_i64, c_i64],
     "oxi_sgd_step": [vp, vp, vp, vp, c_i64, c_float, c_float, c_int],
     "oxi_adamw_step": [vp, vp, vp, vp, vp, c_i64, c_float, c_float, c_float, c_float, c_float, c_int, c_i64],
     "oxi_sgd_step_multi": [vp, c_int, c_float, c_float, c_int],
@@ -164,6 +169,16 @@ class DeviceArray:
         p = vp()
         check(lib.oxi_hip_alloc(self.nbytes, ctypes.byref(p)))
         self.ptr = p.value
+
+    @classmethod
+    def adopt(cls, ptr, shape, dtype=np.float32) -> "DeviceArray":
+        """Wraps a block that liboxihip allocated (freed with oxi_hip_free)."""
+        d = cls.__new__(cls)
+        d.shape = tuple(int(s) for s in shape)
+        d.dtype = np.dtype(dtype)
+        d.nbytes = int(np.prod(d.shape, dtype=np.int64)) * d.dtype.itemsize
+        d.ptr = ptr
+        return d
 
     @classmethod
     def from_numpy(cls, a: np.ndarray) -> "DeviceArray":
@@ -389,6 +404,58 @@ def adamw_step(p: DeviceArray, g: DeviceArray, m: DeviceArray, v: DeviceArray, t
     call("oxi_adamw_step", p.ptr, g.ptr, m.ptr, v.ptr, out.ptr, p.size, lr, beta1, beta2, eps, weight_decay,
          int(bool(decoupled)), t)
     return out
+
+
+def scatter_rows(base: DeviceArray, idx: DeviceArray, values: DeviceArray) -> DeviceArray:
+    """Tensor::scatter_dim0 on a contiguous base: rows idx[p] <- values[p], last write wins."""
+    rows = base.shape[0]
+    inner = int(np.prod(base.shape[1:], dtype=np.int64))
+    out = DeviceArray(base.shape)
+    call("oxi_scatter_rows", base.ptr, rows, inner, idx.ptr, idx.size, values.ptr, out.ptr)
+    return out
+
+
+def scatter_rows_bwd(g: DeviceArray, idx: DeviceArray, values_shape, need_base=True, need_values=True):
+    rows = g.shape[0]
+    inner = int(np.prod(g.shape[1:], dtype=np.int64))
+    gb = DeviceArray(g.shape) if need_base else None
+    gv = DeviceArray(values_shape) if need_values else None
+    call("oxi_scatter_rows_bwd", g.ptr, rows, inner, idx.ptr, idx.size, gb.ptr if gb else None, gv.ptr if gv else None)
+    return gb, gv
+
+
+def broadcast_elem_strides(shape, grid):
+    """Row-major element strides of a contiguous `shape`, expanded to `grid`
+    with 0 on broadcast (missing or size-1) dims."""
+    rm = row_major_strides(shape)
+    lead = len(grid) - len(shape)
+    return [0 if d < lead or shape[d - lead] == 1 else rm[d - lead] for d in range(len(grid))]
+
+
+def masked_select_record(grid) -> DeviceArray:
+    """A device buffer for the record of a selection over `grid`."""
+    nb = c_i64(0)
+    call("oxi_masked_select_record_bytes", _i64arr(grid), len(grid), ctypes.byref(nb))
+    return DeviceArray((nb.value,), np.uint8)
+
+
+def masked_select(x: DeviceArray, mask: DeviceArray, record: DeviceArray | None = None) -> DeviceArray:
+    """Tensor::masked_select over the broadcast of contiguous x and mask; the
+    record (for the VJP) goes to `record` when given."""
+    grid = tuple(np.broadcast_shapes(x.shape, mask.shape))
+    out, cnt = vp(), c_i64(0)
+    call("oxi_masked_select", x.ptr, _i64arr(broadcast_elem_strides(x.shape, grid)), mask.ptr,
+         _i64arr(broadcast_elem_strides(mask.shape, grid)), _i64arr(grid), len(grid), ctypes.byref(out),
+         ctypes.byref(cnt), record.ptr if record is not None else None)
+    return DeviceArray.adopt(out.value, (cnt.value,))
+
+
+def masked_select_bwd(record: DeviceArray, x_shape, mask_shape, g: DeviceArray) -> DeviceArray:
+    grid = tuple(np.broadcast_shapes(tuple(x_shape), tuple(mask_shape)))
+    gx = DeviceArray(x_shape)
+    call("oxi_masked_select_bwd", record.ptr, _i64arr(grid), len(grid), g.ptr, g.size, gx.ptr,
+         _i64arr(broadcast_elem_strides(tuple(x_shape), grid)), gx.size)
+    return gx
 
 
 class SgdSlice(ctypes.Structure):

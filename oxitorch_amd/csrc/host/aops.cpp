@@ -288,6 +288,61 @@ Var index_select(const Var& x, int64_t dim, const std::vector<int64_t>& indices)
   });
 }
 
+// aops::scatter_dim0 (crates/oxi-autograd/src/ops.rs:531-600): the written
+// rows of base get no gradient, the last writer of each row gets that row's.
+Var scatter_dim0(const Var& base, const std::vector<int64_t>& indices, const Var& values) {
+  Tensor out = t_scatter_dim0(base.value(), indices, values.value());
+  const Shape bs = base.value().shape;
+  const Shape vs = values.value().shape;
+  const int64_t rows = bs[0];
+  int64_t inner = 1;
+  for (size_t d = 1; d < bs.size(); ++d) inner *= bs[d];
+  auto ids = device_i64(resolve_indices(indices, rows, 0));
+  const int64_t n = (int64_t)indices.size();
+  return Var::op(out, "scatter_dim0", {base, values},
+                 [bs, vs, rows, inner, ids, n](const Tensor& g, const std::vector<bool>& need) -> Grads {
+                   std::optional<Tensor> gb, gv;
+                   if (need[0]) gb = Tensor::empty(bs, Dev::Hip);
+                   if (need[1]) gv = Tensor::empty(vs, Dev::Hip);
+                   if (gb || gv) {
+                     Tensor gc = t_contiguous(g);
+                     hip_check(oxi_scatter_rows_bwd(gc.data(), rows, inner, static_cast<const int64_t*>(ids->ptr), n,
+                                                    gb ? gb->data() : nullptr, gv ? gv->data() : nullptr));
+                   }
+                   return {gb, gv};
+                 });
+}
+
+// aops::masked_select (crates/oxi-autograd/src/ops.rs:609-667): each pick's
+// gradient goes back to its x element, accumulating over broadcast points.
+// The VJP keeps the forward's selection record (one bit per grid point)
+// instead of x and the mask.
+Var masked_select(const Var& x, const Var& mask) {
+  const bool record = is_grad_enabled() && x.requires_grad();
+  std::shared_ptr<Storage> rec;
+  Tensor out = t_masked_select(x.value(), mask.value(), record ? &rec : nullptr);
+  const Shape xshape = x.value().shape;
+  const Shape grid = broadcast_shapes(xshape, mask.value().shape);
+  const int64_t count = out.numel();
+  return Var::op(out, "masked_select", {x},
+                 [rec, xshape, grid, count](const Tensor& g, const std::vector<bool>& need) -> Grads {
+                   if (!need[0]) return {std::nullopt};
+                   if (!rec) err_other("masked_select: the forward kept no selection record");
+                   // row-major strides of x's own shape on the grid, 0 where x
+                   // broadcasts (a missing or size-1 dim): x_flat_str, ops.rs:628-634
+                   const Shape rm = row_major_strides(xshape);
+                   const size_t lead = grid.size() - xshape.size();
+                   Shape gxs(grid.size(), 0);
+                   for (size_t d = lead; d < grid.size(); ++d)
+                     if (xshape[d - lead] != 1) gxs[d] = rm[d - lead];
+                   Tensor gc = t_contiguous(g);
+                   Tensor gx = Tensor::empty(xshape, Dev::Hip);
+                   hip_check(oxi_masked_select_bwd(rec->ptr, grid.data(), (int)grid.size(), gc.data(), count,
+                                                   gx.data(), gxs.data(), gx.numel()));
+                   return {gx};
+                 });
+}
+
 Var embedding(const std::vector<int64_t>& indices, const Var& weight) {
   return index_select(weight, 0, indices);
 }

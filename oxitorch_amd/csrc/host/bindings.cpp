@@ -415,13 +415,17 @@ PYBIND11_MODULE(_native, m) {
       .def("select", &select_impl)
       .def("index_select", &index_select_impl)
       .def("gather", [](const PyTensor& s, const std::vector<int64_t>& idx) { return index_select_impl(s, 0, idx); })
+      // bindings lib.rs:650-673: differentiable when either operand needs a gradient
       .def("scatter",
-           [](const PyTensor&, const std::vector<int64_t>&, const PyTensor&) -> PyTensor {
-             err_notimpl("scatter is outside this build's device hot path");
+           [](const PyTensor& s, const std::vector<int64_t>& idx, const PyTensor& values) {
+             if (s.v.requires_grad() || values.v.requires_grad())
+               return PyTensor(aops::scatter_dim0(s.v, idx, values.v));
+             return leaf(t_scatter_dim0(s.value(), idx, values.value()));
            })
       .def("masked_select",
-           [](const PyTensor&, const PyTensor&) -> PyTensor {
-             err_notimpl("masked_select is outside this build's device hot path");
+           [](const PyTensor& s, const PyTensor& mask) {
+             if (s.v.requires_grad() || mask.v.requires_grad()) return PyTensor(aops::masked_select(s.v, mask.v));
+             return leaf(t_masked_select(s.value(), mask.value()));
            })
       .def("contiguous", [](const PyTensor& s) { return leaf(t_contiguous(s.value())); })
       .def("apply", &apply)

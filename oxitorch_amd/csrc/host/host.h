@@ -70,6 +70,8 @@ struct Storage {
   ~Storage();
   Storage(const Storage&) = delete;
   Storage& operator=(const Storage&) = delete;
+  // Takes ownership of a device block from oxi_hip_alloc (freed with oxi_hip_free).
+  static std::shared_ptr<Storage> adopt_device(void* ptr, size_t bytes);
 };
 
 class Tensor {
@@ -137,6 +139,12 @@ std::vector<int64_t> resolve_indices(const std::vector<int64_t>& idx, int64_t le
 Tensor t_index_select(const Tensor& t, int64_t dim, const std::vector<int64_t>& indices);
 // Copies `src` into the (possibly strided) view `dst` of the same shape.
 void t_copy_into(const Tensor& dst, const Tensor& src);
+// Tensor::scatter_dim0 (lib.rs:895-932): rows indices[p] of `base` replaced by
+// values[p], last write wins; the reference's argument checks and messages.
+Tensor t_scatter_dim0(const Tensor& base, const std::vector<int64_t>& indices, const Tensor& values);
+// Tensor::masked_select (lib.rs:939-961): 1-D picks over the broadcast grid.
+// With `record`, also keeps the selection's record for the VJP.
+Tensor t_masked_select(const Tensor& x, const Tensor& mask, std::shared_ptr<Storage>* record = nullptr);
 
 // Strides for an elementwise result: the operands' common dense layout when
 // they all share one (keeps a permuted gradient permuted), else row-major.
@@ -205,6 +213,8 @@ Var transpose(const Var& x);
 Var broadcast_to(const Var& x, const Shape& shape);
 Var narrow(const Var& x, int64_t dim, int64_t lo, int64_t hi, int64_t by);
 Var index_select(const Var& x, int64_t dim, const std::vector<int64_t>& indices);
+Var scatter_dim0(const Var& base, const std::vector<int64_t>& indices, const Var& values);
+Var masked_select(const Var& x, const Var& mask);
 
 // Fused hot-path nodes: one graph node and one kernel per direction.
 enum class NormVjp { Ref = OXI_NORM_VJP_REF, Exact = OXI_NORM_VJP_EXACT };

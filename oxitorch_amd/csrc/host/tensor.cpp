@@ -126,6 +126,13 @@ Storage::Storage(Dev d, size_t bytes) : dev(d), nbytes(bytes) {
   }
 }
 
+std::shared_ptr<Storage> Storage::adopt_device(void* ptr, size_t bytes) {
+  auto s = std::make_shared<Storage>(Dev::Hip, 0);
+  s->ptr = ptr;
+  s->nbytes = ptr ? bytes : 0;
+  return s;
+}
+
 Storage::~Storage() {
   if (!ptr) return;
   if (dev == Dev::Cpu) std::free(ptr);
@@ -491,6 +498,51 @@ Tensor t_index_select(const Tensor& t, int64_t dim, const std::vector<int64_t>& 
   auto ids = device_i64(idx);
   hip_check(oxi_index_select(src.data(), outer, len, inner, static_cast<const int64_t*>(ids->ptr),
                              (int64_t)idx.size(), y.data()));
+  return y;
+}
+
+Tensor t_scatter_dim0(const Tensor& base, const std::vector<int64_t>& indices, const Tensor& values) {
+  if (base.ndim() == 0) err_invalid("scatter_dim0 requires at least a 1-D tensor");
+  Shape expect = base.shape;
+  expect[0] = (int64_t)indices.size();
+  if (values.shape != expect) err_shape(fmt_shape(values.shape), fmt_shape(expect));
+  const int64_t rows = base.shape[0];
+  const std::vector<int64_t> idx = resolve_indices(indices, rows, 0);
+  require_hip(base, "scatter");
+  require_hip(values, "scatter");
+  const Tensor b = t_contiguous(base);
+  const Tensor v = t_contiguous(values);
+  int64_t inner = 1;
+  for (int d = 1; d < base.ndim(); ++d) inner *= base.shape[d];
+  Tensor y = Tensor::empty(base.shape, Dev::Hip);
+  if (y.numel() == 0) return y;
+  auto ids = device_i64(idx);
+  hip_check(oxi_scatter_rows(b.data(), rows, inner, static_cast<const int64_t*>(ids->ptr), (int64_t)idx.size(),
+                             v.data(), y.data()));
+  return y;
+}
+
+Tensor t_masked_select(const Tensor& x, const Tensor& mask, std::shared_ptr<Storage>* record) {
+  const Shape grid = broadcast_shapes(x.shape, mask.shape);
+  const Shape xs = broadcast_strides(x.shape, x.strides, grid);
+  const Shape ms = broadcast_strides(mask.shape, mask.strides, grid);
+  require_hip(x, "masked_select");
+  require_hip(mask, "masked_select");
+  void* rec = nullptr;
+  if (record) {
+    int64_t nb = 0;
+    hip_check(oxi_masked_select_record_bytes(grid.data(), (int)grid.size(), &nb));
+    *record = std::make_shared<Storage>(Dev::Hip, (size_t)nb);
+    rec = (*record)->ptr;
+  }
+  float* picks = nullptr;
+  int64_t count = 0;
+  hip_check(oxi_masked_select(x.data(), xs.data(), mask.data(), ms.data(), grid.data(), (int)grid.size(), &picks,
+                              &count, rec));
+  Tensor y;
+  y.st = Storage::adopt_device(picks, sizeof(float) * (size_t)count);
+  y.shape = {count};
+  y.strides = {1};
   return y;
 }
 

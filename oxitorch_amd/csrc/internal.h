@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 
 #include "oxihip.h"
 
@@ -25,12 +26,11 @@ void ws_free(void* p);
 // Device-side guard flag: kernels that meet an index outside its range set it;
 // oxi_hip_sync() reports it. Pointer to one int in device memory.
 int* guard_flag();
-// Device-side completion counters for "last block done" kernels: a kernel
-// whose blocks each add 1 lets the block that sees gridDim-1 finish the work
-// (no block ever waits), and that block resets the counter to 0 before it
-// exits. All kernels run in order on the library stream, so one counter
-// serves every such kernel. Zero at initialisation.
-unsigned* done_counter();
+// A pinned host int64 that a kernel can store one result to (a data-dependent
+// size, say), read by the host after the stream is synchronised: no copy call.
+// Callers hold readback_mutex() from the launch until the read.
+int64_t* readback_slot();
+std::mutex& readback_mutex();
 // Checks the launch that just happened.
 int check_launch(const char* what);
 

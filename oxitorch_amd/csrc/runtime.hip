@@ -29,7 +29,8 @@ struct Runtime {
   int cus = 0;
   hipStream_t stream = nullptr;
   int* guard = nullptr;  // device int, see guard_flag()
-  unsigned* done = nullptr;  // device counter, see done_counter()
+  int64_t* readback = nullptr;  // pinned host slot, see readback_slot()
+  std::mutex readback_mu;
   // caching allocator state
   std::multimap<size_t, void*> free_blocks;  // rounded size -> block
   std::unordered_map<void*, size_t> live;    // block -> rounded size
@@ -70,9 +71,9 @@ int init_locked(Runtime& r, int device) {
   if ((e = hipMalloc(&r.guard, sizeof(int))) != hipSuccess) return fail_hip(e, "hipMalloc(guard)");
   if ((e = hipMemsetAsync(r.guard, 0, sizeof(int), r.stream)) != hipSuccess)
     return fail_hip(e, "hipMemsetAsync(guard)");
-  if ((e = hipMalloc(&r.done, sizeof(unsigned))) != hipSuccess) return fail_hip(e, "hipMalloc(done counter)");
-  if ((e = hipMemsetAsync(r.done, 0, sizeof(unsigned), r.stream)) != hipSuccess)
-    return fail_hip(e, "hipMemsetAsync(done counter)");
+  if ((e = hipHostMalloc(reinterpret_cast<void**>(&r.readback), sizeof(int64_t), hipHostMallocDefault)) != hipSuccess)
+    return fail_hip(e, "hipHostMalloc(readback)");
+  *r.readback = 0;
   if ((e = hipStreamSynchronize(r.stream)) != hipSuccess) return fail_hip(e, "hipStreamSynchronize");
   r.device = device;
   return OXI_OK;
@@ -109,7 +110,8 @@ bool ensure_init() {
 
 hipStream_t stream() { return rt().stream; }
 int* guard_flag() { return rt().guard; }
-unsigned* done_counter() { return rt().done; }
+int64_t* readback_slot() { return rt().readback; }
+std::mutex& readback_mutex() { return rt().readback_mu; }
 int cu_count() { return rt().cus > 0 ? rt().cus : 256; }
 
 void* ws_alloc(size_t bytes) {

@@ -324,3 +324,28 @@ def test_warmup_then_cosine_sequential():
         op.SequentialLR(o, [warm, cosine], milestones=[])
     with pytest.raises(ValueError):
         op.LinearWarmup(o, warmup_epochs=-1)
+
+
+def test_indexing_argument_checks_before_device(ox):
+    """Tensor::scatter_dim0 / masked_select argument checks (lib.rs:895-942)
+    run on the host with the reference's messages, before any device work."""
+    base = cpu(ox, np.zeros((3, 2)))
+    with pytest.raises(RuntimeError, match="index 3 out of range for dim 0 of size 3"):
+        base.scatter([3], cpu(ox, np.zeros((1, 2))))
+    with pytest.raises(ValueError, match=r"shape mismatch: \[1, 3\] vs \[1, 2\]"):
+        base.scatter([0], cpu(ox, np.zeros((1, 3))))
+    with pytest.raises(ValueError, match="at least a 1-D tensor"):
+        ox.from_numpy(np.float32(1.0).reshape(()), device="cpu").scatter([], cpu(ox, np.zeros((0,))))
+    with pytest.raises(ValueError, match="shape mismatch"):
+        base.masked_select(cpu(ox, np.ones((4,))))
+    with pytest.raises(NotImplementedError, match="on a host"):
+        base.masked_select(cpu(ox, np.ones((3, 2))))
+    from oxitorch_amd import capi
+
+    with pytest.raises(ValueError, match="negative size"):
+        capi.call("oxi_scatter_rows", None, -1, 4, None, 0, None, None)
+    with pytest.raises(ValueError, match="negative size"):
+        capi.call("oxi_masked_select_bwd", None, None, 0, None, -1, None, None, 0)
+    nb = capi.c_i64(0)
+    capi.call("oxi_masked_select_record_bytes", capi._i64arr([16384, 4096]), 2, capi.ctypes.byref(nb))
+    assert nb.value == 8 * (16384 + 1) + 16384 * 4096 // 8  # 4096-element tiles' offsets + one bit per element

@@ -453,3 +453,119 @@ def test_sgd_matches_float64_over_steps():
         bq = 0.9 * bq + g
         q = q - 0.05 * (0.9 * bq)
     assert not np.allclose(p, q, rtol=1e-6, atol=1e-6)
+
+
+# ---- scatter_dim0 and masked_select (crates/oxi-tensor/src/lib.rs:895-961,
+# crates/oxi-autograd/src/ops.rs:531-667) -------------------------------------------
+
+def test_kat_scatter_and_masked_select():
+    """python/tests/test_indexing_grad.py:20-69,111-117."""
+    base = np.array([[10.0, 11.0], [20.0, 21.0], [30.0, 31.0]], np.float32)
+    vals = np.array([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], np.float32)
+    assert ref.scatter_dim0(base, [2, 0, 2], vals).tolist() == [[3.0, 4.0], [20.0, 21.0], [5.0, 6.0]]
+    gb, gv = ref.scatter_dim0_bwd(np.ones((3, 2), np.float32), [2, 0, 2], (3, 2))
+    assert gb.tolist() == [[0.0, 0.0], [1.0, 1.0], [0.0, 0.0]]
+    assert gv.tolist() == [[0.0, 0.0], [1.0, 1.0], [1.0, 1.0]]
+    r = rng(7)
+    a = r.standard_normal((5, 3)).astype(np.float32)
+    v3 = r.standard_normal((3, 3)).astype(np.float32)
+    want = a.copy()
+    want[[4, 1, 4]] = v3
+    assert np.array_equal(ref.scatter_dim0(a, [4, 1, 4], v3), want)
+    assert ref.scatter_dim0(np.ones((2, 2), np.float32), [0], np.full((1, 2), -1.0, np.float32)).tolist() == \
+        [[-1.0, -1.0], [1.0, 1.0]]
+    col = np.array([[7.0], [9.0]], np.float32)
+    mask = np.array([[1.0, 1.0, 0.0], [0.0, 1.0, 1.0]], np.float32)
+    assert ref.masked_select(col, mask).tolist() == [7.0, 7.0, 9.0, 9.0]
+    assert ref.masked_select_bwd(col.shape, mask, np.array([1, 2, 3, 4], np.float32)).tolist() == [[3.0], [7.0]]
+    r = rng(11)
+    a = r.standard_normal((2, 3)).astype(np.float32)
+    up = r.standard_normal((2, 3)).astype(np.float32)
+    m = (r.standard_normal((2, 3)) > 0).astype(np.float32)
+    np.testing.assert_allclose(ref.masked_select_bwd(a.shape, m, up[m > 0]), m * up, rtol=1e-4, atol=1e-5)
+
+
+def _rand_ids(r, rows, n):
+    ids = r.integers(-rows, rows, n)
+    if n:
+        ids[: n // 3] = ids[0]  # a run of duplicates: last-writer logic matters
+    return ids
+
+
+@pytest.mark.parametrize("shape,n", [((7,), 5), ((9, 4), 12), ((6, 3, 5), 10), ((4, 2), 0)])
+def test_scatter_against_numpy_and_adjoint(shape, n):
+    """Forward: numpy's fancy assignment (last write wins). VJP: the adjoint
+    identity <g, S(db, dv)> = <gb, db> + <gv, dv> of the linear map S, in
+    float64; a VJP that credits the first writer instead fails it."""
+    r = rng(100 + n)
+    rows = shape[0]
+    ids = _rand_ids(r, rows, n)
+    base = r.standard_normal(shape).astype(np.float32)
+    vals = r.standard_normal((n,) + shape[1:]).astype(np.float32)
+    want = base.copy()
+    if n:
+        want[ids] = vals
+    got = ref.scatter_dim0(base, ids, vals)
+    assert np.array_equal(got, want)
+    g = r.standard_normal(shape).astype(np.float32)
+    gb, gv = ref.scatter_dim0_bwd(g, ids, vals.shape)
+    db = r.standard_normal(shape)
+    dv = r.standard_normal(vals.shape)
+    lin = ref.scatter_dim0(db.astype(np.float32), ids, dv.astype(np.float32)).astype(np.float64)
+    lhs = float(np.sum(g.astype(np.float64) * lin))
+    rhs = float(np.sum(gb * db.astype(np.float32).astype(np.float64)) +
+                np.sum(gv * dv.astype(np.float32).astype(np.float64)))
+    assert abs(lhs - rhs) <= 1e-9 * (1 + abs(lhs))
+    if n:
+        # planted mistake: credit the FIRST writer of each row
+        bad = np.zeros_like(gv)
+        seen = set()
+        for p, i in enumerate(ids % rows):
+            if i not in seen:
+                bad[p] = g[i]
+                seen.add(i)
+        rhs_bad = float(np.sum(gb * db.astype(np.float32)) + np.sum(bad * dv.astype(np.float32)))
+        if not np.array_equal(bad, gv):
+            assert abs(lhs - rhs_bad) > 1e-6 * (1 + abs(lhs))
+
+
+def test_scatter_bwd_signed_zero_and_nan():
+    """gbase is g * 0 on written rows: -0 for a negative g, NaN for a NaN g."""
+    g = np.array([[-1.0, np.nan], [2.0, -3.0]], np.float32)
+    gb, _ = ref.scatter_dim0_bwd(g, [0], (1, 2))
+    assert np.signbit(gb[0, 0]) and gb[0, 0] == 0 and np.isnan(gb[0, 1])
+    assert gb[1].tolist() == [2.0, -3.0]
+
+
+@pytest.mark.parametrize("xs,ms", [((3, 4), (3, 4)), ((2, 1, 5), (3, 5)), ((4,), (3, 1)), ((1,), (2, 3)),
+                                   ((2, 3, 4), (4,))])
+def test_masked_select_against_numpy_and_adjoint(xs, ms):
+    """Forward: numpy boolean indexing of the broadcast arrays. VJP: np.add.at
+    over the broadcast positions (exact here: few adds per element) and the
+    adjoint identity of the linear map x -> masked_select(x, m)."""
+    r = rng(200 + len(xs) + len(ms))
+    x = r.standard_normal(xs).astype(np.float32)
+    m = (r.random(ms) > 0.4).astype(np.float32)
+    m.ravel()[0] = -0.0  # negative zero is not picked
+    m.ravel()[-1] = np.nan  # NaN compares != 0: picked
+    grid = np.broadcast_shapes(xs, ms)
+    xb, mb = np.broadcast_to(x, grid), np.broadcast_to(m, grid)
+    sel = mb != 0
+    assert np.array_equal(ref.masked_select(x, m), xb[sel])
+    g = r.standard_normal(int(sel.sum())).astype(np.float32)
+    gx = ref.masked_select_bwd(xs, m, g)
+    pos = np.broadcast_to(np.arange(x.size).reshape(xs), grid)[sel]
+    want = np.zeros(x.size, np.float64)
+    np.add.at(want, pos, g.astype(np.float64))
+    np.testing.assert_allclose(gx.ravel(), want, rtol=1e-6, atol=1e-6)
+    dx = r.standard_normal(xs).astype(np.float32)
+    lhs = float(np.sum(g.astype(np.float64) * ref.masked_select(dx, m)))
+    rhs = float(np.sum(gx.astype(np.float64) * dx))
+    assert abs(lhs - rhs) <= 1e-5 * (1 + abs(lhs))
+
+
+def test_masked_select_drops_nan_values():
+    """The reference's NaN marker also drops picked NaN values of x."""
+    x = np.array([1.0, np.nan, 3.0], np.float32)
+    m = np.ones(3, np.float32)
+    assert ref.masked_select(x, m).tolist() == [1.0, 3.0]
