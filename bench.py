@@ -6,7 +6,8 @@ of synthetic, seeded input that is already resident in HBM, driven through the
 liboxihip C-ABI (include/oxihip.h) in the order the host core launches it.
 Default workload: config 2, F.layer_norm(affine) -> exact-erf gelu, fwd+bwd,
 fp32, x (16384, 4096). `--config c1|c3|c4|c5` selects the other configs;
-`--config f3` times masked_select and the row scatter (fwd+bwd), and
+`--config f2` times device DataLoader batches (the step before the path),
+`--config f3` masked_select and the row scatter (fwd+bwd), and
 `--config f4` one AdamW step over GPT-2 small's 148 parameter tensors (the
 optimizer step after backward).
 
@@ -384,6 +385,76 @@ class F4(Workload):
         ref.adamw_step(h["p"][lo:hi], h["g"][lo:hi], m, v, 10, *self.hyper)
 
 
+class F2(Workload):
+    """The input pipeline: shuffled batches of 8192 rows from an MNIST-shaped
+    dataset (60000 x 784 features + labels, fp32) resident in HBM, drawn
+    through the host core's DataLoader (one device gather per column per
+    batch, the epoch's order uploaded once). Side figures: 256 MiB host->device
+    and device->host through the pinned staging ring and through plain
+    waiting copies."""
+
+    def __init__(self, hip):
+        super().__init__(hip)
+        import oxitorch_amd as ox
+        from oxitorch_amd import _native
+
+        N, D, B = 60000, 784, 8192
+        self.N, self.Dm, self.B = N, D, B
+        self.name = "F2 device DataLoader, MNIST-shaped (60000,784)+labels fp32, shuffled batches of 8192 rows"
+        r = np.random.default_rng(22)
+        x = r.standard_normal((N, D), dtype=np.float32)
+        y = r.integers(0, 10, N).astype(np.float32)
+        self.host = dict(x=x, y=y)
+        self.loader = _native.DataLoader([ox.from_numpy(x), ox.from_numpy(y)], batch_size=B, shuffle=True,
+                                         drop_last=True, seed=5)
+        self.it = iter(self.loader)
+        self.rows = B
+        self.perm = np.random.RandomState(5).permutation(N)
+        # per batch: each row read and written once per column, plus its id
+        self.bytes_per_step = 2 * B * (D + 1) * 4 + 2 * B * 8
+        self.keep = None
+
+    def _batch(self):
+        try:
+            self.keep = next(self.it)
+        except StopIteration:
+            self.it = iter(self.loader)
+            self.keep = next(self.it)
+
+    def kernels(self):
+        return [("loader_batch", self._batch, self.bytes_per_step)]
+
+    def side_figures(self):
+        """PCIe rates of 256 MiB copies (GB/s)."""
+        hip = self.hip
+        nb = 256 << 20
+        a = np.random.default_rng(1).integers(0, 255, nb, dtype=np.uint8)
+        back = np.empty_like(a)
+        d = hip.DeviceArray((nb,), np.uint8)
+        out = {}
+        for label, fn in [("upload_staged", lambda: hip.call("oxi_hip_upload", d.ptr, a.ctypes.data, nb)),
+                          ("h2d_waiting_copy", lambda: hip.call("oxi_hip_memcpy_h2d", d.ptr, a.ctypes.data, nb)),
+                          ("download_staged", lambda: hip.call("oxi_hip_download", back.ctypes.data, d.ptr, nb)),
+                          ("d2h_waiting_copy", lambda: hip.call("oxi_hip_memcpy_d2h", back.ctypes.data, d.ptr, nb))]:
+            fn()
+            hip.sync()
+            t0 = time.perf_counter()
+            for _ in range(5):
+                fn()
+            hip.sync()
+            out[label] = round(5 * nb / (time.perf_counter() - t0) / 1e9, 2)
+        assert np.array_equal(back, a)
+        d.free()
+        return out
+
+    def cpu_step(self, ref, lo, hi):
+        # the reference's worker path: host index_select of the batch rows
+        h = self.host
+        ids = self.perm[lo % self.N:lo % self.N + (hi - lo)]
+        ref.index_select(h["x"], 0, ids)
+        ref.index_select(h["y"].reshape(-1, 1), 0, ids)
+
+
 class F3(Workload):
     """The remaining indexing ops, fwd+bwd: masked_select over x (16384, 4096)
     with a density-0.5 mask of the same shape, and the last-write-wins row
@@ -458,7 +529,7 @@ class F3(Workload):
         ref.scatter_dim0_bwd(h["gs"], h["ids"], h["vals"].shape)
 
 
-WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f3": F3, "f4": F4}
+WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f2": F2, "f3": F3, "f4": F4}
 
 
 # ---------------------------------------------------------------------------
@@ -598,6 +669,8 @@ def main():
                      "algorithmic_bytes": d["bytes"]},
         "cpu_baseline": None,
     }
+    if hasattr(wl, "side_figures"):
+        line["pcie_gbs"] = wl.side_figures()
     if hasattr(wl, "per_tensor"):
         alt = wl.per_tensor()
         ms_alt = time_steps(hip, alt, max(3, min(args.steps, 10)))

@@ -102,6 +102,24 @@ int oxi_hip_memory_stats(size_t* in_use, size_t* cached);
 int oxi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int oxi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int oxi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Transfers that do not stall the library stream (the step before the hot
+ * path: ids, targets and loader batches reaching the device). Replaces the
+ * CPU-only movement of Tensor::to / .cpu() and the loader's host batches
+ * (plan.md:266-268; crates/oxi-data/src/batch.rs:411-423). */
+/* Page-locked host memory; oxi_hip_host_free waits for queued copies first. */
+int oxi_hip_host_alloc(size_t bytes, void** out);
+int oxi_hip_host_free(void* ptr);
+/* Upload from any host memory: the bytes are copied into a pinned staging
+ * ring and the DMA is queued on the library stream; returns as soon as `src`
+ * may be reused, without waiting for the device. */
+int oxi_hip_upload(void* dst, const void* src, size_t bytes);
+/* Queue a DMA from page-locked memory (oxi_hip_host_alloc) on the library
+ * stream without waiting; `pinned_src` must stay unchanged until the stream
+ * has passed the copy (oxi_hip_sync, or an event). */
+int oxi_hip_memcpy_h2d_async(void* dst, const void* pinned_src, size_t bytes);
+/* Download through the pinned ring, chunked and double-buffered; waits for
+ * the queued work and the copy. */
+int oxi_hip_download(void* dst, const void* src, size_t bytes);
 /* Wait for all queued work; reports a pending device-side guard (e.g. an id
  * that escaped host validation) as OXI_OUT_OF_BOUNDS. */
 int oxi_hip_sync(void);

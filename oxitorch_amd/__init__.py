@@ -25,7 +25,7 @@ from oxitorch_amd._native import (  # noqa: F401
     version,
     zeros,
 )
-from oxitorch_amd import nn, optim  # noqa: E402
+from oxitorch_amd import nn, optim, utils  # noqa: E402
 
 __all__ = [
     "Tensor",
@@ -41,6 +41,7 @@ __all__ = [
     "nn",
     "no_grad",
     "optim",
+    "utils",
     "set_default_device",
     "set_grad_enabled",
     "synchronize",

@@ -39,7 +39,7 @@ HIP_FLAGS = [
     f"-I{CSRC}",
 ]
 
-HIP_SOURCES = ["runtime.hip", "elementwise.hip", "norm.hip", "softmax.hip", "reduce.hip", "embedding.hip", "indexing.hip", "optim.hip"]
+HIP_SOURCES = ["runtime.hip", "elementwise.hip", "norm.hip", "softmax.hip", "reduce.hip", "embedding.hip", "indexing.hip", "optim.hip", "transfer.hip"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -59,6 +59,11 @@ _SIGS = {
     "oxi_hip_memcpy_h2d": [vp, vp, c_size],
     "oxi_hip_memcpy_d2h": [vp, vp, c_size],
     "oxi_hip_memcpy_d2d": [vp, vp, c_size],
+    "oxi_hip_host_alloc": [c_size, ctypes.POINTER(vp)],
+    "oxi_hip_host_free": [vp],
+    "oxi_hip_upload": [vp, vp, c_size],
+    "oxi_hip_memcpy_h2d_async": [vp, vp, c_size],
+    "oxi_hip_download": [vp, vp, c_size],
     "oxi_hip_sync": [],
     "oxi_hip_stream": [ctypes.POINTER(vp)],
     "oxi_hip_event_create": [ctypes.POINTER(vp)],

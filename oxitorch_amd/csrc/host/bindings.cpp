@@ -536,6 +536,43 @@ PYBIND11_MODULE(_native, m) {
     return leaf(t_binary_op("min", a, t_scalar_full(t.shape, hi, t.dev())));
   });
 
+  // ---- tensor-column loader (bindings data.rs:115-365): columns live in HBM,
+  // batches are device gathers in the epoch's (optionally shuffled) order
+  py::class_<LoaderIter>(m, "LoaderIter")
+      .def("__iter__", [](py::object self) { return self; })
+      .def("__next__", [](LoaderIter& it) {
+        std::vector<Tensor> cols;
+        if (!it.next(&cols)) throw py::stop_iteration();
+        py::list out;
+        for (Tensor& t : cols) out.append(py::cast(leaf(std::move(t))));
+        return out;
+      });
+  py::class_<Loader>(m, "DataLoader")
+      .def(py::init([](const py::list& columns, int64_t batch_size, bool shuffle, bool drop_last,
+                       std::optional<uint64_t> seed, int64_t num_workers, const py::object& transforms,
+                       uint64_t transform_seed) {
+             if (!transforms.is_none())
+               err_notimpl("native batch transforms (crop/flip/normalize) are outside this build's device path");
+             (void)transform_seed;
+             std::vector<Tensor> cols;
+             for (const py::handle& c : columns) {
+               if (!py::isinstance<PyTensor>(c)) throw py::type_error("DataLoader columns must be oxitorch.Tensor");
+               cols.push_back(c.cast<PyTensor&>().value());
+             }
+             if (batch_size < 0 || num_workers < 0) throw py::value_error("batch_size and num_workers must be >= 0");
+             return Loader(cols, batch_size, shuffle, drop_last, seed, num_workers);
+           }),
+           py::arg("columns"), py::arg("batch_size") = 1, py::arg("shuffle") = false, py::arg("drop_last") = false,
+           py::arg("seed") = py::none(), py::arg("num_workers") = 0, py::arg("transforms") = py::none(),
+           py::arg("transform_seed") = 0)
+      .def_property_readonly("n", &Loader::n)
+      .def_property_readonly("batch_size", &Loader::batch_size)
+      .def("__iter__", &Loader::iter);
+  // NumPy RandomState(seed).permutation(n), as the loader shuffles
+  m.def("_mt19937_permutation", [](uint32_t seed, int64_t n) { return Mt19937(seed).permutation(n); });
+  // epoch_plan (batch.rs:269-292) as (start, length) pairs
+  m.def("_epoch_plan", &epoch_plan);
+
   // ---- optimizers (bindings lib.rs:807-936): state lives in the host core,
   // each step rebinds the given Tensor objects to their updated leaves.
   py::class_<Sgd>(m, "RustSgd")

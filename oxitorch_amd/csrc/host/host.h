@@ -10,6 +10,7 @@
 
 #include <cstdint>
 #include <functional>
+#include <future>
 #include <memory>
 #include <mutex>
 #include <optional>
@@ -41,6 +42,7 @@ class Error : public std::exception {
 [[noreturn]] void err_notimpl(const std::string& m);                      // "not implemented: m"
 [[noreturn]] void err_oob(const std::string& m);                          // "out of bounds: m"
 [[noreturn]] void err_other(const std::string& m);                        // "m"
+[[noreturn]] void err_invalid_plain(const std::string& m);                // ValueError "m" (no prefix)
 // Raises the Error matching an oxi_status, with liboxihip's message.
 void hip_check(int rc);
 
@@ -262,6 +264,55 @@ class AdamW {
   bool decoupled_;
   std::vector<std::optional<Tensor>> moments_, sq_moments_;
   std::vector<uint64_t> steps_;
+};
+
+// ---- tensor-column loader (crates/oxi-data, crates/oxi-bindings/src/data.rs) ------
+
+// MT19937 with NumPy RandomState(seed) streams (crates/oxi-data/src/rng.rs).
+class Mt19937 {
+ public:
+  explicit Mt19937(uint32_t seed);
+  uint32_t next_u32();
+  uint64_t below(uint64_t bound);                // uniform in [0, bound), NumPy's masked rejection
+  std::vector<int64_t> permutation(int64_t n);   // RandomState.permutation(n)
+
+ private:
+  void twist();
+  uint32_t mt_[624];
+  int mti_;
+};
+
+// (start, length) of each batch of an epoch over n rows (batch.rs:269-292).
+std::vector<std::pair<int64_t, int64_t>> epoch_plan(int64_t n, int64_t batch_size, bool drop_last);
+
+struct LoaderIter {
+  std::vector<Tensor> columns;
+  std::shared_ptr<Storage> order;  // this epoch's row order, int64 on the device
+  std::vector<std::pair<int64_t, int64_t>> batches;
+  size_t pos = 0;
+  bool next(std::vector<Tensor>* out);  // false once the epoch is done
+};
+
+class Loader {
+ public:
+  Loader(const std::vector<Tensor>& columns, int64_t batch_size, bool shuffle, bool drop_last,
+         std::optional<uint64_t> seed, int64_t num_workers);
+  int64_t n() const { return n_; }
+  int64_t batch_size() const { return batch_size_; }
+  LoaderIter iter();
+
+ private:
+  std::vector<int64_t> next_order();
+  void prefetch_order();
+  std::vector<Tensor> columns_;  // contiguous, device-resident
+  // the next shuffled epoch's order, computed on a host thread while the
+  // current epoch runs (the permutation is the loader's only host work)
+  std::future<std::vector<int64_t>> pending_;
+  int64_t n_ = 0, batch_size_ = 1;
+  bool shuffle_ = false, drop_last_ = false;
+  std::optional<uint64_t> seed_;
+  uint64_t epoch_ = 0;
+  int64_t workers_ = 0;
 };
 
 }  // namespace oxt

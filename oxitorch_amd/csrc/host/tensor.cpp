@@ -20,6 +20,7 @@ void err_shape(const std::string& l, const std::string& r) {
 void err_notimpl(const std::string& m) { throw Error(ErrKind::NotImplemented, "not implemented: " + m); }
 void err_oob(const std::string& m) { throw Error(ErrKind::OutOfBounds, "out of bounds: " + m); }
 void err_other(const std::string& m) { throw Error(ErrKind::Other, m); }
+void err_invalid_plain(const std::string& m) { throw Error(ErrKind::InvalidArgument, m); }
 
 void hip_check(int rc) {
   if (rc == OXI_OK) return;
@@ -190,7 +191,7 @@ Tensor t_from_host(const float* data, const Shape& shape, Dev d) {
   const size_t bytes = sizeof(float) * (size_t)t.numel();
   if (!bytes) return t;
   if (d == Dev::Cpu) std::memcpy(t.data(), data, bytes);
-  else hip_check(oxi_hip_memcpy_h2d(t.data(), data, bytes));
+  else hip_check(oxi_hip_upload(t.data(), data, bytes));  // staged, no stream wait
   return t;
 }
 
@@ -200,7 +201,9 @@ std::vector<float> t_to_host(const Tensor& t) {
   if (n == 0) return out;
   if (t.dev() == Dev::Hip) {
     Tensor c = t_contiguous(t);
-    hip_check(oxi_hip_memcpy_d2h(out.data(), c.data(), sizeof(float) * (size_t)n));
+    // staged through the pinned ring: double-buffered chunks beat a plain
+    // waiting copy from pageable memory
+    hip_check(oxi_hip_download(out.data(), c.data(), sizeof(float) * (size_t)n));
     return out;
   }
   // host: walk the strides row-major (iterate::map_n general path)
@@ -477,7 +480,7 @@ std::vector<int64_t> resolve_indices(const std::vector<int64_t>& idx, int64_t le
 
 std::shared_ptr<Storage> device_i64(const std::vector<int64_t>& v) {
   auto s = std::make_shared<Storage>(Dev::Hip, sizeof(int64_t) * v.size());
-  if (!v.empty()) hip_check(oxi_hip_memcpy_h2d(s->ptr, v.data(), sizeof(int64_t) * v.size()));
+  if (!v.empty()) hip_check(oxi_hip_upload(s->ptr, v.data(), sizeof(int64_t) * v.size()));
   return s;
 }
 

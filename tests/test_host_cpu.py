@@ -349,3 +349,50 @@ def test_indexing_argument_checks_before_device(ox):
     nb = capi.c_i64(0)
     capi.call("oxi_masked_select_record_bytes", capi._i64arr([16384, 4096]), 2, capi.ctypes.byref(nb))
     assert nb.value == 8 * (16384 + 1) + 16384 * 4096 // 8  # 4096-element tiles' offsets + one bit per element
+
+
+# ---- input pipeline host logic (crates/oxi-data/src/{rng,batch}.rs) -------------------
+
+def test_mt19937_permutation_matches_numpy(ox):
+    """rng.rs:131-141 (the recorded NumPy stream) and NumPy itself for several
+    seeds and sizes, including the loader's 32-bit seed truncation range."""
+    from oxitorch_amd import _native
+
+    assert _native._mt19937_permutation(7, 10) == [8, 5, 0, 2, 1, 9, 7, 3, 6, 4]
+    for seed in (0, 1, 42, 2**31 + 5, 2**32 - 1):
+        for n in (1, 2, 17, 1000, 65537):
+            want = np.random.RandomState(seed).permutation(n).tolist()
+            assert _native._mt19937_permutation(seed, n) == want, (seed, n)
+
+
+def test_epoch_plan(ox):
+    """batch.rs:430-460: sequential chunks with a remainder; drop_last drops
+    only a short tail and keeps a lone short batch; batch size 0 rejected."""
+    from oxitorch_amd import _native
+
+    assert _native._epoch_plan(12, 5, False) == [(0, 5), (5, 5), (10, 2)]
+    assert _native._epoch_plan(12, 5, True) == [(0, 5), (5, 5)]
+    assert _native._epoch_plan(3, 5, True) == [(0, 3)]
+    assert _native._epoch_plan(10, 5, True) == [(0, 5), (5, 5)]
+    with pytest.raises(ValueError, match="batch_size must be >= 1"):
+        _native._epoch_plan(4, 0, False)
+
+
+def test_loader_argument_checks(ox):
+    """bindings data.rs:149-176, before any device work."""
+    from oxitorch_amd import _native
+
+    with pytest.raises(ValueError, match="at least one tensor column"):
+        _native.DataLoader([])
+    with pytest.raises(ValueError, match="dataset is empty"):
+        _native.DataLoader([cpu(ox, np.zeros((0, 2)))])
+    with pytest.raises(ValueError, match="batch_size must be >= 1"):
+        _native.DataLoader([cpu(ox, np.zeros((3, 2)))], batch_size=0)
+    with pytest.raises(ValueError, match="column 1 has 2 rows, expected 3"):
+        _native.DataLoader([cpu(ox, np.zeros((3, 2))), cpu(ox, np.zeros((2,)))])
+    with pytest.raises(NotImplementedError, match="transforms"):
+        _native.DataLoader([cpu(ox, np.zeros((3, 2)))], transforms=object())
+    from oxitorch_amd.utils.data import DataLoader, TensorDataset
+
+    with pytest.raises(ValueError, match="batch_size must be >= 1"):
+        DataLoader(TensorDataset(cpu(ox, np.zeros((3, 2)))), batch_size=0)
