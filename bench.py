@@ -561,6 +561,24 @@ def time_kernels(hip, kernels, reps):
     return out
 
 
+def time_cold(hip, kernels, reps=20, flush_bytes=512 << 20):
+    """Median step time with cold caches: before each step, a 512 MiB fill
+    (twice the 256 MB Infinity Cache) evicts the step's inputs; the step alone
+    is timed with HIP events on the library stream."""
+    scratch = hip.DeviceArray((flush_bytes // 4,))
+    t = hip.Timer()
+    times = []
+    for _ in range(reps):
+        hip.check(hip.lib.oxi_fill(scratch.ptr, flush_bytes // 4, 0.0))
+        t.start()
+        for _, fn, _ in kernels:
+            fn()
+        times.append(t.stop())
+    scratch.free()
+    times.sort()
+    return times[len(times) // 2]
+
+
 def copy_probe(hip, nbytes=1 << 30):
     """STREAM-style copy rates (read + write bytes) on this GPU."""
     a = hip.DeviceArray((nbytes // 4,))
@@ -580,6 +598,27 @@ def copy_probe(hip, nbytes=1 << 30):
     a.free()
     b.free()
     return res
+
+
+def _cpu_threads():
+    """Host threads for the threaded baseline: the box's CPU share (at most 16)."""
+    return max(1, min(os.cpu_count() or 1, 16))
+
+
+def cpu_threaded(wl, ref, budget_s, threads):
+    """Row chunks of the same workload on `threads` host threads (the oracle's
+    C calls release the GIL); returns (rows, seconds)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    chunk = max(1, min(wl.rows // threads, 1024))
+    t0 = time.perf_counter()
+    done = 0
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        while time.perf_counter() - t0 < budget_s:
+            starts = [((done + k * chunk) % wl.rows) for k in range(threads)]
+            list(pool.map(lambda lo: wl.cpu_step(ref, lo, min(lo + chunk, wl.rows)), starts))
+            done += sum(min(lo + chunk, wl.rows) - lo for lo in starts)
+    return done, time.perf_counter() - t0
 
 
 def cpu_baseline(wl, budget_s):
@@ -608,15 +647,30 @@ def cpu_baseline(wl, budget_s):
             done += min(n, wl.rows - lo)
     el = time.perf_counter() - t0
     bytes_per_row = wl.bytes_per_step / wl.rows
-    return {
-        "value": round(done * bytes_per_row / el / 1e9, 4),
+    one = {"value": round(done * bytes_per_row / el / 1e9, 4), "rows_per_s": round(done / el, 1),
+           "sample": f"{done} of {wl.rows} rows, {el:.2f} s"}
+    out = {
+        "value": one["value"],
         "unit": "GB/s",
-        "rows_per_s": round(done / el, 1),
+        "rows_per_s": one["rows_per_s"],
         "cores": 1,
         "kind": "port",
         "sample": f"{done} of {wl.rows} rows of the same workload, fwd+bwd through oracle/refcpu.c "
                   f"(single thread), {el:.2f} s; GB/s scaled by the same algorithmic bytes per row",
     }
+    threads = _cpu_threads()
+    if threads > 1 and not (isinstance(wl, (C4, C5)) or getattr(wl, "cpu_full", False)):
+        # row-parallel like the reference's rayon row reductions (its
+        # elementwise passes run on one thread, so this is the faster of the two)
+        n, secs = cpu_threaded(wl, ref, budget_s, threads)
+        out["single_thread"] = one
+        out["value"] = round(n * bytes_per_row / secs / 1e9, 4)
+        out["rows_per_s"] = round(n / secs, 1)
+        out["cores"] = threads
+        out["sample"] = (f"row chunks of the same workload on {threads} host threads through oracle/refcpu.c, "
+                         f"{n} rows in {secs:.2f} s (single thread: {one['sample']}); GB/s scaled by the same "
+                         "algorithmic bytes per row")
+    return out
 
 
 def main():
@@ -669,6 +723,17 @@ def main():
                      "algorithmic_bytes": d["bytes"]},
         "cpu_baseline": None,
     }
+    log("cold-cache median")
+    ms_cold = time_cold(hip, kernels)
+    line["cold_cache"] = {"ms_per_step_median_of_20": round(ms_cold, 5),
+                          "gbs": round(wl.bytes_per_step / (ms_cold * 1e-3) / 1e9, 2),
+                          "protocol": "512 MiB fill before each timed step"}
+    props = hip.device_props()
+    # HBM3E moves 4 bits per pin per reported memory clock (8 Gb/s per pin at
+    # 2 GHz), so clock x 4 x bus width is the interface peak the props imply
+    line["device"] = dict(props, peak_from_props_gbs=round(
+        props["memory_clock_khz"] * 1e3 * 4 * props["memory_bus_bits"] / 8 / 1e9, 1),
+        peak_datasheet_gbs=PEAK_HBM_GBS)
     if hasattr(wl, "side_figures"):
         line["pcie_gbs"] = wl.side_figures()
     if hasattr(wl, "per_tensor"):

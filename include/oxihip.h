@@ -132,6 +132,18 @@ int oxi_hip_event_create(void** event);
 int oxi_hip_event_record(void* event);
 int oxi_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 int oxi_hip_event_destroy(void* event);
+/* Properties of the initialised device, for reports (memory clock and bus
+ * width as the runtime gives them; the HBM peak they imply is the caller's
+ * to derive). */
+typedef struct oxi_device_props {
+  int32_t compute_units;
+  int32_t memory_clock_khz;
+  int32_t memory_bus_bits;
+  int32_t l2_bytes;
+  int64_t hbm_bytes;
+  char arch[64];
+} oxi_device_props;
+int oxi_hip_device_props(oxi_device_props* out);
 /* Test hook: make the next `n`-th allocation fail (0 disables). */
 int oxi_hip_debug_fail_alloc_after(int n);
 

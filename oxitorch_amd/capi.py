@@ -71,6 +71,7 @@ _SIGS = {
     "oxi_hip_event_elapsed_ms": [vp, vp, ctypes.POINTER(c_float)],
     "oxi_hip_event_destroy": [vp],
     "oxi_hip_debug_fail_alloc_after": [c_int],
+    "oxi_hip_device_props": [vp],
     "oxi_fill": [vp, c_i64, c_float],
     "oxi_unary": [c_int, vp, P_i64, vp, P_i64, P_i64, c_int],
     "oxi_binary": [c_int, vp, P_i64, vp, P_i64, vp, P_i64, P_i64, c_int],
@@ -213,6 +214,21 @@ class DeviceArray:
             self.free()
         except Exception:
             pass
+
+
+class DeviceProps(ctypes.Structure):
+    """oxi_device_props"""
+    _fields_ = [("compute_units", ctypes.c_int32), ("memory_clock_khz", ctypes.c_int32),
+                ("memory_bus_bits", ctypes.c_int32), ("l2_bytes", ctypes.c_int32), ("hbm_bytes", ctypes.c_int64),
+                ("arch", ctypes.c_char * 64)]
+
+
+def device_props() -> dict:
+    p = DeviceProps()
+    call("oxi_hip_device_props", ctypes.byref(p))
+    return {"compute_units": p.compute_units, "memory_clock_khz": p.memory_clock_khz,
+            "memory_bus_bits": p.memory_bus_bits, "l2_bytes": p.l2_bytes, "hbm_bytes": p.hbm_bytes,
+            "arch": p.arch.decode()}
 
 
 def row_major_strides(shape):

@@ -305,6 +305,22 @@ int oxi_hip_event_destroy(void* ev) {
   return err == hipSuccess ? OXI_OK : fail_hip(err, "hipEventDestroy");
 }
 
+int oxi_hip_device_props(oxi_device_props* out) {
+  if (!out) return fail(OXI_INVALID_ARGUMENT, "device_props: out must not be NULL");
+  OXI_CHECK_INIT();
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, rt().device);
+  if (e != hipSuccess) return fail_hip(e, "hipGetDeviceProperties");
+  std::memset(out, 0, sizeof *out);
+  out->compute_units = p.multiProcessorCount;
+  out->memory_clock_khz = p.memoryClockRate;
+  out->memory_bus_bits = p.memoryBusWidth;
+  out->l2_bytes = p.l2CacheSize;
+  out->hbm_bytes = (int64_t)p.totalGlobalMem;
+  std::snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+  return OXI_OK;
+}
+
 int oxi_hip_debug_fail_alloc_after(int n) {
   Runtime& r = rt();
   std::lock_guard<std::mutex> lk(r.mu);
