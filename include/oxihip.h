@@ -127,7 +127,8 @@ int oxi_hip_sync(void);
 const char* oxi_hip_last_error(void);
 /* The library stream (a hipStream_t), for callers that time or order work. */
 int oxi_hip_stream(void** stream);
-/* Events on the library stream, for timing kernels. */
+/* Events on the library stream, for timing kernels (created without the
+ * system-scope fence, which would flush the caches at every record). */
 int oxi_hip_event_create(void** event);
 int oxi_hip_event_record(void* event);
 int oxi_hip_event_elapsed_ms(void* start, void* stop, float* ms);
@@ -254,6 +255,20 @@ int oxi_index_select(const float* src, int64_t outer, int64_t len, int64_t inner
  * (crates/oxi-autograd/src/ops.rs:741-769). */
 int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inner,
                          const int64_t* idx, int64_t n, float* grad_src);
+/* The same VJP in two halves, so the id-dependent half leaves the backward:
+ * _plan sorts the ids (a stable sort by id with each id's presence flag) on
+ * the library's second stream, after everything already queued on the library
+ * stream, as soon as the ids are known (at forward time); _apply makes the
+ * library stream wait for the plan and runs the segment sums of g for any
+ * (outer, inner) of the same ids. A plan may be applied more than once.
+ * _plan_free releases it (after the library stream has passed its sort).
+ * Together they compute exactly what oxi_index_select_bwd computes. The
+ * plan/apply split has no counterpart in the reference (its VJP is one call,
+ * scatter_index_select, crates/oxi-autograd/src/ops.rs:741-769). */
+int oxi_index_select_bwd_plan(const int64_t* idx, int64_t n, int64_t len, void** plan);
+int oxi_index_select_bwd_apply(const void* plan, const float* g, int64_t outer, int64_t inner,
+                               float* grad_src);
+int oxi_index_select_bwd_plan_free(void* plan);
 /* F.embedding (functional.py:245-247) = index_select on dim 0 of W (V, D). */
 int oxi_embedding_fwd(const float* W, const int64_t* ids, int64_t n,
                       int64_t V, int64_t D, float* out);

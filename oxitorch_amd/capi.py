@@ -91,6 +91,9 @@ _SIGS = {
     "oxi_cross_entropy_bwd": [vp, vp, vp, vp, vp, c_i64, c_i64],
     "oxi_index_select": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
     "oxi_index_select_bwd": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
+    "oxi_index_select_bwd_plan": [vp, c_i64, c_i64, ctypes.POINTER(vp)],
+    "oxi_index_select_bwd_apply": [vp, vp, c_i64, c_i64, vp],
+    "oxi_index_select_bwd_plan_free": [vp],
     "oxi_embedding_fwd": [vp, vp, c_i64, c_i64, c_i64, vp],
     "oxi_embedding_bwd": [vp, vp, c_i64, c_i64, c_i64, vp],
     "oxi_reduce": [c_int, vp, P_i64, P_i64, c_int, c_int, vp],
@@ -383,6 +386,33 @@ def index_select_bwd(g: DeviceArray, full_shape, dim: int, idx: DeviceArray) -> 
     grad = DeviceArray(full_shape)
     call("oxi_index_select_bwd", g.ptr, o, l, i, idx.ptr, idx.size, grad.ptr)
     return grad
+
+
+class BwdPlan:
+    """The id sort of an index_select VJP, queued on the library's second
+    stream (oxi_index_select_bwd_plan); freed with the object."""
+
+    def __init__(self, idx: DeviceArray, length: int):
+        p = vp()
+        call("oxi_index_select_bwd_plan", idx.ptr, idx.size, length, ctypes.byref(p))
+        self.ptr = p.value
+
+    def apply(self, g: DeviceArray, full_shape, dim: int) -> DeviceArray:
+        o, _, i = _oli(tuple(full_shape), dim)
+        grad = DeviceArray(full_shape)
+        call("oxi_index_select_bwd_apply", self.ptr, g.ptr, o, i, grad.ptr)
+        return grad
+
+    def free(self):
+        if self.ptr:
+            lib.oxi_index_select_bwd_plan_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 def embedding_fwd(W: DeviceArray, ids: DeviceArray) -> DeviceArray:

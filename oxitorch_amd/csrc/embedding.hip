@@ -588,6 +588,125 @@ int check_sizes(const char* what, int64_t outer, int64_t len, int64_t inner, int
   return OXI_OK;
 }
 
+// The id-dependent half of the VJP: the stable sort of (key, position)
+// pairs and each key's presence flag. Built on any stream; `ready` is set
+// when it was built on the side stream.
+struct SortPlan {
+  int64_t n = 0, len = 0;
+  void* ws = nullptr;  // keys, pos, keys2, pos2, count table, present, owner count
+  const int* ka = nullptr;  // sorted keys and their positions
+  const int* va = nullptr;
+  int* present = nullptr;
+  int* owner_count = nullptr;  // zeroed by the sort; counts long-key owners in an apply
+  hipEvent_t queued = nullptr;  // the library stream's position when the plan was queued
+  hipEvent_t ready = nullptr;   // recorded on the side stream after the sort
+  mutable int applies = 0;  // a second apply (retain_graph) re-zeroes the owner count
+  bool recorded = false;    // `ready` holds the sort's completion
+};
+
+int build_plan(const int64_t* idx, int64_t n, int64_t len, hipStream_t s, SortPlan* p) {
+  p->n = n;
+  p->len = len;
+  if (n == 0) return OXI_OK;
+  if (len + 1 >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: dim too large");
+  // sort tiles: 2, 8 or 32 elements per thread, so that tables stay within
+  // SELF_SCAN_MAX tiles up to 2M indices
+  const int ipt = n <= 65536 ? 2 : (n <= 524288 ? 8 : 32);
+  const int64_t rtiles = ceil_div(n, (int64_t)SBS * ipt);
+  if (rtiles * 256 >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many indices");
+  int passes = 0;
+  for (int64_t m = len; m > 0; m >>= 8) ++passes;  // keys are in [0, len]
+  if (passes == 0) passes = 1;
+  const size_t ints = 4 * (size_t)n + 256 * (size_t)rtiles + (size_t)len + 1;
+  p->ws = ws_alloc(ints * sizeof(int));
+  if (!p->ws) return OXI_OTHER;
+  int* keys = static_cast<int*>(p->ws);
+  int* pos = keys + n;
+  int* keys2 = pos + n;
+  int* pos2 = keys2 + n;
+  int* tab = pos2 + n;
+  p->present = tab + 256 * rtiles;
+  p->owner_count = p->present + len;
+  // pass p reads (ka, va) and writes (kb, vb); pass 0 reads the ids
+  const int* ka = nullptr;
+  const int* va = nullptr;
+  int* bufk[2] = {keys, keys2};
+  int* bufv[2] = {pos, pos2};
+  for (int ps = 0; ps < passes; ++ps) {
+    int* kb = bufk[ps & 1];
+    int* vb = bufv[ps & 1];
+    if (ipt == 2) sort_pass<2>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, p->present, p->owner_count);
+    else if (ipt == 8) sort_pass<8>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, p->present, p->owner_count);
+    else sort_pass<32>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, p->present, p->owner_count);
+    ka = kb;
+    va = vb;
+  }
+  p->ka = ka;
+  p->va = va;
+  return check_launch("index_select_bwd/sort");
+}
+
+// The gradient half, on the library stream: segment sums of g's rows in the
+// plan's order, zero rows for absent keys, the fix-up of long keys.
+int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, float* grad) {
+  const int64_t n = p.n, len = p.len;
+  const int64_t total_out = outer * len * inner;
+  if (total_out == 0) return OXI_OK;
+  if (!grad) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: NULL output pointer");
+  if (n == 0) return oxi_fill(grad, total_out, 0.f);
+  if (!g) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: NULL tensor pointer");
+  hipStream_t s = stream();
+  // segment tiles: as long as possible (fewer cut runs) while still giving
+  // every CU several waves
+  const bool vec = inner % 4 == 0 && al16(g) && al16(grad);
+  const int64_t units = vec ? inner / 4 : inner;
+  const int64_t chunks = ceil_div(units, 64);
+  const int64_t c16 = ceil_div(units, 16);
+  if (c16 >= (1 << 24)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: rows too wide");
+  int st = 64;
+  while (st > 16 && ceil_div(n, st) * chunks < 8 * (int64_t)cu_count()) st >>= 1;
+  const int64_t stiles = ceil_div(n, st);
+  // end tile per key and the owner list of long keys; partial rows
+  Workspace wsi(((size_t)len + (size_t)stiles) * sizeof(int));
+  Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(float));
+  if (!wsi.p || !wsp.p) return OXI_OTHER;
+  int* end_tile = wsi.as<int>();
+  int* owners = end_tile + len;
+  const int* ka = p.ka;
+  const int* va = p.va;
+  int* present = p.present;
+  int* owner_count = p.owner_count;
+  if (p.applies++ > 0) {
+    if (int rc = oxi_fill(reinterpret_cast<float*>(owner_count), 1, 0.0f)) return rc;  // 0.0f is all-zero bits
+  }
+  float* part = wsp.as<float>();
+  const int64_t seg_blocks = ceil_div(stiles * chunks, 4);
+  // the rows of g stream through the cache while dW is written: decide on
+  // the launch's whole traffic, not on dW alone
+  const bool nts = nt_stores((total_out + outer * n * inner) * 4);
+  const int64_t blocks = seg_blocks + ceil_div(len, ZR);
+  if (blocks >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many rows");
+  const dim3 sg((unsigned)blocks), st256(256);
+  if (vec && nts)
+    seg_wave_k<true, true><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners, owner_count,
+                                                end_tile, st, stiles, (int)chunks, seg_blocks);
+  else if (vec)
+    seg_wave_k<true, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
+                                                 owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
+  else
+    seg_wave_k<false, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
+                                                  owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
+  if (int rc = check_launch("index_select_bwd/segments")) return rc;
+  const unsigned fb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(stiles * c16, 4 * (int64_t)cu_count()));
+  if (vec)
+    seg_fixup_k<true><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
+                                         grad, (int)c16, guard_flag());
+  else
+    seg_fixup_k<false><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
+                                          grad, (int)c16, guard_flag());
+  return check_launch("index_select_bwd/fixup");
+}
+
 }  // namespace
 }  // namespace oxi
 
@@ -624,6 +743,69 @@ int oxi_index_select(const float* src, int64_t outer, int64_t len, int64_t inner
   return check_launch("index_select");
 }
 
+int oxi_index_select_bwd_plan(const int64_t* idx, int64_t n, int64_t len, void** plan) {
+  if (!plan) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd_plan: NULL plan");
+  *plan = nullptr;
+  if (int rc = check_sizes("index_select_bwd_plan", 1, len, 1, n)) return rc;
+  if (n > 0 && !idx) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd_plan: NULL ids");
+  OXI_CHECK_INIT();
+  SortPlan* p = new SortPlan();
+  // the side stream starts after everything already queued on the library
+  // stream: the ids' upload, and every earlier user of the plan's memory
+  p->queued = take_event();
+  p->ready = take_event();
+  if (!p->queued || !p->ready) {
+    (void)oxi_index_select_bwd_plan_free(p);
+    return fail(OXI_OTHER, "index_select_bwd_plan: no event available");
+  }
+  hipError_t e = hipEventRecord(p->queued, stream());
+  if (e == hipSuccess) e = hipStreamWaitEvent(side_stream(), p->queued, 0);
+  if (e != hipSuccess) {
+    (void)oxi_index_select_bwd_plan_free(p);
+    return fail_hip(e, "index_select_bwd_plan: ordering the side stream");
+  }
+  int rc = build_plan(idx, n, len, side_stream(), p);
+  if (rc == OXI_OK) {
+    e = hipEventRecord(p->ready, side_stream());
+    if (e != hipSuccess) rc = fail_hip(e, "index_select_bwd_plan: recording the plan");
+    else p->recorded = true;
+  }
+  if (rc != OXI_OK) {
+    (void)oxi_index_select_bwd_plan_free(p);
+    return rc;
+  }
+  *plan = p;
+  return OXI_OK;
+}
+
+int oxi_index_select_bwd_apply(const void* plan, const float* g, int64_t outer, int64_t inner, float* grad) {
+  if (!plan) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd_apply: NULL plan");
+  const SortPlan& p = *static_cast<const SortPlan*>(plan);
+  if (int rc = check_sizes("index_select_bwd_apply", outer, p.len, inner, p.n)) return rc;
+  OXI_CHECK_INIT();
+  // a cross-stream wait costs a barrier packet on the library stream: skip it
+  // when the sort has already finished
+  if (p.recorded && hipEventQuery(p.ready) != hipSuccess) {
+    hipError_t e = hipStreamWaitEvent(stream(), p.ready, 0);
+    if (e != hipSuccess) return fail_hip(e, "index_select_bwd_apply: waiting for the plan");
+  }
+  return apply_plan(p, g, outer, inner, grad);
+}
+
+int oxi_index_select_bwd_plan_free(void* plan) {
+  if (!plan) return OXI_OK;
+  SortPlan* p = static_cast<SortPlan*>(plan);
+  // the library stream passes the plan's sort before its memory can be
+  // reused, and before its events go back to the pool
+  if (p->recorded && ensure_init() && hipEventQuery(p->ready) != hipSuccess)
+    (void)hipStreamWaitEvent(stream(), p->ready, 0);
+  if (p->ws) ws_free(p->ws);
+  give_event(p->queued);
+  give_event(p->ready);
+  delete p;
+  return OXI_OK;
+}
+
 int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inner, const int64_t* idx, int64_t n,
                          float* grad) {
   if (int rc = check_sizes("index_select_bwd", outer, len, inner, n)) return rc;
@@ -633,82 +815,12 @@ int oxi_index_select_bwd(const float* g, int64_t outer, int64_t len, int64_t inn
   OXI_CHECK_INIT();
   if (n == 0) return oxi_fill(grad, total_out, 0.f);
   if (!g || !idx) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: NULL tensor pointer");
-  if (len + 1 >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: dim too large");
-  hipStream_t s = stream();
-  // sort tiles: 2, 8 or 32 elements per thread, so that tables stay within
-  // SELF_SCAN_MAX tiles up to 2M indices
-  const int ipt = n <= 65536 ? 2 : (n <= 524288 ? 8 : 32);
-  const int64_t rtiles = ceil_div(n, (int64_t)SBS * ipt);
-  if (rtiles * 256 >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many indices");
-  int passes = 0;
-  for (int64_t m = len; m > 0; m >>= 8) ++passes;  // keys are in [0, len]
-  if (passes == 0) passes = 1;
-  // segment tiles: as long as possible (fewer cut runs) while still giving
-  // every CU several waves
-  const bool vec = inner % 4 == 0 && al16(g) && al16(grad);
-  const int64_t units = vec ? inner / 4 : inner;
-  const int64_t chunks = ceil_div(units, 64);
-  const int64_t c16 = ceil_div(units, 16);
-  if (c16 >= (1 << 24)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: rows too wide");
-  int st = 64;
-  while (st > 16 && ceil_div(n, st) * chunks < 8 * (int64_t)cu_count()) st >>= 1;
-  const int64_t stiles = ceil_div(n, st);
-  // workspace (ints): keys, pos, keys2, pos2 (n each), count table
-  // (256 * rtiles), present (len), end_tile (len), owners (stiles), owner count
-  const size_t ints = 4 * (size_t)n + 256 * (size_t)rtiles + 2 * (size_t)len + (size_t)stiles + 1;
-  Workspace wsi(ints * sizeof(int));
-  Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(float));
-  if (!wsi.p || !wsp.p) return OXI_OTHER;
-  int* keys = wsi.as<int>();
-  int* pos = keys + n;
-  int* keys2 = pos + n;
-  int* pos2 = keys2 + n;
-  int* tab = pos2 + n;
-  int* present = tab + 256 * rtiles;
-  int* end_tile = present + len;
-  int* owners = end_tile + len;
-  int* owner_count = owners + stiles;
-  // pass p reads (ka, va) and writes (kb, vb); pass 0 reads the ids
-  const int* ka = nullptr;
-  const int* va = nullptr;
-  int* bufk[2] = {keys, keys2};
-  int* bufv[2] = {pos, pos2};
-  for (int ps = 0; ps < passes; ++ps) {
-    int* kb = bufk[ps & 1];
-    int* vb = bufv[ps & 1];
-    if (ipt == 2) sort_pass<2>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
-    else if (ipt == 8) sort_pass<8>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
-    else sort_pass<32>(s, ps, n, len, (int)rtiles, idx, ka, va, kb, vb, tab, present, owner_count);
-    ka = kb;
-    va = vb;
-  }
-  if (int rc = check_launch("index_select_bwd/sort")) return rc;
-  float* part = wsp.as<float>();
-  const int64_t seg_blocks = ceil_div(stiles * chunks, 4);
-  // the rows of g stream through the cache while dW is written: decide on
-  // the launch's whole traffic, not on dW alone
-  const bool nts = nt_stores((total_out + outer * n * inner) * 4);
-  const int64_t blocks = seg_blocks + ceil_div(len, ZR);
-  if (blocks >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many rows");
-  const dim3 sg((unsigned)blocks), st256(256);
-  if (vec && nts)
-    seg_wave_k<true, true><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners, owner_count,
-                                                end_tile, st, stiles, (int)chunks, seg_blocks);
-  else if (vec)
-    seg_wave_k<true, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
-                                                 owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
-  else
-    seg_wave_k<false, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
-                                                  owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
-  if (int rc = check_launch("index_select_bwd/segments")) return rc;
-  const unsigned fb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(stiles * c16, 4 * (int64_t)cu_count()));
-  if (vec)
-    seg_fixup_k<true><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
-                                         grad, (int)c16, guard_flag());
-  else
-    seg_fixup_k<false><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
-                                          grad, (int)c16, guard_flag());
-  return check_launch("index_select_bwd/fixup");
+  // the whole VJP on the library stream
+  SortPlan p;
+  int rc = build_plan(idx, n, len, stream(), &p);
+  if (rc == OXI_OK) rc = apply_plan(p, g, outer, inner, grad);
+  if (p.ws) ws_free(p.ws);
+  return rc;
 }
 
 int oxi_embedding_fwd(const float* W, const int64_t* ids, int64_t n, int64_t V, int64_t D, float* out) {

@@ -269,21 +269,29 @@ Var narrow(const Var& x, int64_t dim, int64_t lo, int64_t hi, int64_t by) {
 
 // ---- index_select (ops.rs:498-517, 741-769) -----------------------------------------
 
+// The VJP's id sort is queued at forward time on the library's second stream
+// (oxi_index_select_bwd_plan), where it overlaps the rest of the forward; the
+// backward only waits for it and runs the segment sums.
 Var index_select(const Var& x, int64_t dim, const std::vector<int64_t>& indices) {
-  Tensor out = t_index_select(x.value(), dim, indices);
+  if (!is_grad_enabled() || !x.requires_grad()) return Var::leaf(t_index_select(x.value(), dim, indices), false);
+  if (x.value().ndim() == 0) err_invalid("dim " + std::to_string(dim) + " out of range for 0-D tensor");
   const int d = normalize_dim(dim, x.value().ndim());
   const Shape xs = x.value().shape;
   auto ids = device_i64(resolve_indices(indices, xs[d], d));
   const int64_t n = (int64_t)indices.size();
-  return Var::op(out, "index_select", {x}, [xs, d, ids, n](const Tensor& g, const std::vector<bool>& need) -> Grads {
+  // the sort is queued first so that it overlaps the gather itself
+  void* raw = nullptr;
+  hip_check(oxi_index_select_bwd_plan(static_cast<const int64_t*>(ids->ptr), n, xs[d], &raw));
+  std::shared_ptr<void> plan(raw, [ids](void* p) { (void)oxi_index_select_bwd_plan_free(p); });
+  Tensor out = t_index_select_dev(x.value(), d, ids, n);
+  return Var::op(out, "index_select", {x}, [xs, d, plan](const Tensor& g, const std::vector<bool>& need) -> Grads {
     if (!need[0]) return {std::nullopt};
     Tensor gc = t_contiguous(g);
     int64_t outer = 1, inner = 1;
     for (int i = 0; i < d; ++i) outer *= xs[i];
     for (size_t i = d + 1; i < xs.size(); ++i) inner *= xs[i];
     Tensor grad = Tensor::empty(xs, Dev::Hip);
-    hip_check(oxi_index_select_bwd(gc.data(), outer, xs[d], inner, static_cast<const int64_t*>(ids->ptr), n,
-                                   grad.data()));
+    hip_check(oxi_index_select_bwd_apply(plan.get(), gc.data(), outer, inner, grad.data()));
     return {grad};
   });
 }

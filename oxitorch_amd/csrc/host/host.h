@@ -139,6 +139,8 @@ Tensor t_reduce_all(Reduce kind, const Tensor& t);
 // Validates all indices first (negative wrap); OutOfBounds with the reference text.
 std::vector<int64_t> resolve_indices(const std::vector<int64_t>& idx, int64_t len, int dim);
 Tensor t_index_select(const Tensor& t, int64_t dim, const std::vector<int64_t>& indices);
+// index_select along normalized dim `d` with ids already on the device (resolved, n of them).
+Tensor t_index_select_dev(const Tensor& t, int d, const std::shared_ptr<Storage>& ids, int64_t n);
 // Copies `src` into the (possibly strided) view `dst` of the same shape.
 void t_copy_into(const Tensor& dst, const Tensor& src);
 // Tensor::scatter_dim0 (lib.rs:895-932): rows indices[p] of `base` replaced by

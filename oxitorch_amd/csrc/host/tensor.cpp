@@ -484,24 +484,27 @@ std::shared_ptr<Storage> device_i64(const std::vector<int64_t>& v) {
   return s;
 }
 
-Tensor t_index_select(const Tensor& t, int64_t dim, const std::vector<int64_t>& indices) {
-  if (t.ndim() == 0) err_invalid("dim " + std::to_string(dim) + " out of range for 0-D tensor");
-  const int d = normalize_dim(dim, t.ndim());
-  const int64_t len = t.shape[d];
-  const std::vector<int64_t> idx = resolve_indices(indices, len, d);
+Tensor t_index_select_dev(const Tensor& t, int d, const std::shared_ptr<Storage>& ids, int64_t n) {
   require_hip(t, "index_select");
   const Tensor src = t_contiguous(t);
   int64_t outer = 1, inner = 1;
   for (int i = 0; i < d; ++i) outer *= t.shape[i];
   for (int i = d + 1; i < t.ndim(); ++i) inner *= t.shape[i];
   Shape out_shape = t.shape;
-  out_shape[d] = (int64_t)idx.size();
+  out_shape[d] = n;
   Tensor y = Tensor::empty(out_shape, Dev::Hip);
   if (y.numel() == 0) return y;
-  auto ids = device_i64(idx);
-  hip_check(oxi_index_select(src.data(), outer, len, inner, static_cast<const int64_t*>(ids->ptr),
-                             (int64_t)idx.size(), y.data()));
+  hip_check(oxi_index_select(src.data(), outer, t.shape[d], inner, static_cast<const int64_t*>(ids->ptr), n,
+                             y.data()));
   return y;
+}
+
+Tensor t_index_select(const Tensor& t, int64_t dim, const std::vector<int64_t>& indices) {
+  if (t.ndim() == 0) err_invalid("dim " + std::to_string(dim) + " out of range for 0-D tensor");
+  const int d = normalize_dim(dim, t.ndim());
+  const std::vector<int64_t> idx = resolve_indices(indices, t.shape[d], d);
+  require_hip(t, "index_select");
+  return t_index_select_dev(t, d, device_i64(idx), (int64_t)idx.size());
 }
 
 Tensor t_scatter_dim0(const Tensor& base, const std::vector<int64_t>& indices, const Tensor& values) {

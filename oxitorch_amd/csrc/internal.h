@@ -20,6 +20,18 @@ int fail_hip(hipError_t err, const char* what);
 // Returns nullptr and sets the error when no device can be initialised.
 bool ensure_init();
 hipStream_t stream();
+// A second stream, default priority, for work that overlaps the library
+// stream (e.g. the embedding VJP's id sort queued at forward time). Work on
+// it first waits for an event recorded on the library stream, and the
+// library stream waits for an event recorded after it, so memory from the
+// stream-ordered allocator stays safe.
+hipStream_t side_stream();
+// Ordering events without timing, pooled: give_event() returns one for reuse
+// instead of destroying it, because destroying an event the device has not
+// reached yet can make the host wait for it. Re-recording a pooled event is
+// safe once every wait on its previous record has been queued.
+hipEvent_t take_event();
+void give_event(hipEvent_t e);
 // Workspace from the caching allocator (stream-ordered reuse, no sync).
 void* ws_alloc(size_t bytes);
 void ws_free(void* p);

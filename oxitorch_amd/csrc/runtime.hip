@@ -28,6 +28,7 @@ struct Runtime {
   int device = -1;
   int cus = 0;
   hipStream_t stream = nullptr;
+  hipStream_t side = nullptr;  // default priority, see side_stream()
   int* guard = nullptr;  // device int, see guard_flag()
   int64_t* readback = nullptr;  // pinned host slot, see readback_slot()
   std::mutex readback_mu;
@@ -37,6 +38,7 @@ struct Runtime {
   size_t bytes_in_use = 0;
   size_t bytes_cached = 0;
   int fail_after = 0;  // debug hook
+  std::vector<hipEvent_t> events;  // pooled ordering events, see take_event()
 };
 
 Runtime& rt() {
@@ -68,6 +70,8 @@ int init_locked(Runtime& r, int device) {
   r.cus = prop.multiProcessorCount;
   if ((e = hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking)) != hipSuccess)
     return fail_hip(e, "hipStreamCreateWithFlags");
+  if ((e = hipStreamCreateWithFlags(&r.side, hipStreamNonBlocking)) != hipSuccess)
+    return fail_hip(e, "hipStreamCreateWithFlags(side)");
   if ((e = hipMalloc(&r.guard, sizeof(int))) != hipSuccess) return fail_hip(e, "hipMalloc(guard)");
   if ((e = hipMemsetAsync(r.guard, 0, sizeof(int), r.stream)) != hipSuccess)
     return fail_hip(e, "hipMemsetAsync(guard)");
@@ -109,6 +113,31 @@ bool ensure_init() {
 }
 
 hipStream_t stream() { return rt().stream; }
+hipStream_t side_stream() { return rt().side; }
+
+hipEvent_t take_event() {
+  Runtime& r = rt();
+  {
+    std::lock_guard<std::mutex> lk(r.mu);
+    if (!r.events.empty()) {
+      hipEvent_t e = r.events.back();
+      r.events.pop_back();
+      return e;
+    }
+  }
+  // device-scope release: both streams work on device memory, and a default
+  // (system-scope) record writes back and invalidates the caches each time
+  hipEvent_t e = nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventReleaseToDevice) != hipSuccess) return nullptr;
+  return e;
+}
+
+void give_event(hipEvent_t e) {
+  if (!e) return;
+  Runtime& r = rt();
+  std::lock_guard<std::mutex> lk(r.mu);
+  r.events.push_back(e);
+}
 int* guard_flag() { return rt().guard; }
 int64_t* readback_slot() { return rt().readback; }
 std::mutex& readback_mutex() { return rt().readback_mu; }
@@ -176,6 +205,7 @@ int oxi_hip_alloc(size_t bytes, void** out) {
       (void)hipGetLastError();
       // Give the cache back to the driver and retry once. The stream must be
       // idle before blocks are released to the driver.
+      (void)hipStreamSynchronize(r.side);
       (void)hipStreamSynchronize(r.stream);
       release_cache_locked(r);
       e = hipMalloc(&p, sz);
@@ -208,6 +238,7 @@ int oxi_hip_free(void* ptr) {
 int oxi_hip_empty_cache(void) {
   Runtime& r = rt();
   std::lock_guard<std::mutex> lk(r.mu);
+  if (r.side) (void)hipStreamSynchronize(r.side);
   if (r.stream) (void)hipStreamSynchronize(r.stream);
   release_cache_locked(r);
   return OXI_OK;
@@ -253,7 +284,8 @@ int oxi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
 
 int oxi_hip_sync(void) {
   OXI_CHECK_INIT();
-  hipError_t e = hipStreamSynchronize(stream());
+  hipError_t e = hipStreamSynchronize(side_stream());
+  if (e == hipSuccess) e = hipStreamSynchronize(stream());
   if (e != hipSuccess) return fail_hip(e, "hipStreamSynchronize");
   int flag = 0;
   e = hipMemcpy(&flag, guard_flag(), sizeof(int), hipMemcpyDeviceToHost);
@@ -278,9 +310,11 @@ int oxi_hip_stream(void** s) {
 int oxi_hip_event_create(void** ev) {
   if (!ev) return fail(OXI_INVALID_ARGUMENT, "event must not be NULL");
   OXI_CHECK_INIT();
+  // timing only: no system-scope fence, which would write back and
+  // invalidate the caches at every record and perturb the kernels timed
   hipEvent_t e;
-  hipError_t err = hipEventCreate(&e);
-  if (err != hipSuccess) return fail_hip(err, "hipEventCreate");
+  hipError_t err = hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
+  if (err != hipSuccess) return fail_hip(err, "hipEventCreateWithFlags");
   *ev = (void*)e;
   return OXI_OK;
 }

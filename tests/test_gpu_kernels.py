@@ -366,6 +366,38 @@ def test_index_select_bwd_run_shapes(hip, case):
     assert_reduction_close(got, want32, exact, what=f"index_select_bwd {case}")
 
 
+@pytest.mark.parametrize("case", ["skewed_outer", "zipf_vocab", "empty"])
+def test_index_select_bwd_plan_matches_one_call(hip, case):
+    """The sort plan queued on the second stream, applied (twice, as a second
+    backward would), equals the one-call VJP bit for bit; a plan freed
+    without being applied leaves the stream usable."""
+    say("index_select_bwd plan", case)
+    r = rng(31)
+    if case == "skewed_outer":
+        shape, dim = (4, 6, 130), 1
+        idx = np.minimum(r.zipf(1.3, 500) - 1, 5).astype(np.int64)
+    elif case == "zipf_vocab":
+        shape, dim = (50257, 64), 0
+        idx = np.minimum(r.zipf(1.1, 20000) - 1, 50256).astype(np.int64)
+    else:
+        shape, dim = (30, 8), 0
+        idx = np.zeros(0, np.int64)
+    out_shape = list(shape)
+    out_shape[dim] = idx.size
+    g = r.standard_normal(out_shape).astype(np.float32)
+    dg, di = D(hip, g), D(hip, idx) if idx.size else hip.DeviceArray((0,), np.int64)
+    want = hip.index_select_bwd(dg, shape, dim, di).numpy()
+    plan = hip.BwdPlan(di, shape[dim])
+    first = plan.apply(dg, shape, dim).numpy()
+    second = plan.apply(dg, shape, dim).numpy()
+    plan.free()
+    np.testing.assert_array_equal(first, want)
+    np.testing.assert_array_equal(second, want)
+    unused = hip.BwdPlan(di, shape[dim])
+    unused.free()
+    hip.sync()
+
+
 def _zipf_ids(seed, shape, V):
     r = rng(seed)
     return np.minimum(r.zipf(1.1, shape) - 1, V - 1).astype(np.int64)
