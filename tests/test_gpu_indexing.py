@@ -112,7 +112,9 @@ def _grid_strides(shape, grid):
 
 MASK_CASES = [((3, 4), (3, 4), 0.5), ((2, 1, 5), (3, 5), 0.6), ((4,), (3, 1), 0.5), ((1,), (2, 3), 0.5),
               ((2, 3, 4), (4,), 0.5), ((4097,), (4097,), 0.3), ((16384, 4096), (16384, 4096), 0.5),
-              ((1000, 1), (1000, 777), 0.1), ((64, 1, 33), (1, 50, 33), 0.9), ((5,), (5,), 0.0), ((3,), (3,), 1.0)]
+              ((1000, 1), (1000, 777), 0.1), ((64, 1, 33), (1, 50, 33), 0.9), ((5,), (5,), 0.0), ((3,), (3,), 1.0),
+              # hundreds of 4096-point tiles with no pick or all picked
+              ((1200000,), (1200000,), 0.0), ((1200000,), (1200000,), 0.00002), ((700, 3000), (700, 3000), 1.0)]
 
 
 @pytest.mark.parametrize("xs,ms,density", MASK_CASES)
