@@ -415,7 +415,7 @@ class F4(Workload):
 class F2(Workload):
     """The input pipeline: shuffled batches of 8192 rows from an MNIST-shaped
     dataset (60000 x 784 features + labels, fp32) resident in HBM, drawn
-    through the host core's DataLoader (one device gather per column per
+    through the host core's DataLoader (one device gather of all columns per
     batch, the epoch's order uploaded once). Side figures: 256 MiB host->device
     and device->host through the pinned staging ring and through plain
     waiting copies."""
@@ -427,13 +427,15 @@ class F2(Workload):
 
         N, D, B = 60000, 784, 8192
         self.N, self.Dm, self.B = N, D, B
-        self.name = "F2 device DataLoader, MNIST-shaped (60000,784)+labels fp32, shuffled batches of 8192 rows"
+        self.name = ("F2 device DataLoader, MNIST-shaped (60000,784)+labels fp32, shuffled batches of 8192 rows, "
+                     "num_workers=4")
         r = np.random.default_rng(22)
         x = r.standard_normal((N, D), dtype=np.float32)
         y = r.integers(0, 10, N).astype(np.float32)
         self.host = dict(x=x, y=y)
+        # four host threads compute the coming epochs' orders (the only host work)
         self.loader = _native.DataLoader([ox.from_numpy(x), ox.from_numpy(y)], batch_size=B, shuffle=True,
-                                         drop_last=True, seed=5)
+                                         drop_last=True, seed=5, num_workers=4)
         self.it = iter(self.loader)
         self.rows = B
         self.perm = np.random.RandomState(5).permutation(N)

@@ -269,6 +269,19 @@ int oxi_index_select_bwd_plan(const int64_t* idx, int64_t n, int64_t len, void**
 int oxi_index_select_bwd_apply(const void* plan, const float* g, int64_t outer, int64_t inner,
                                float* grad_src);
 int oxi_index_select_bwd_plan_free(void* plan);
+
+/* One batch of a column-tensor loader: dst[k, i] = src[idx[k], i] for every
+ * column (src contiguous (len, inner), dst (n, inner)), all columns in one
+ * launch (more than 8 columns take one launch per 8). Replaces
+ * gather_columns (crates/oxi-data/src/batch.rs:406-423: index_select(0,
+ * indices) per column). Ids in [-len, len) wrap; the caller validates them,
+ * this kernel only guards (see oxi_hip_sync). */
+typedef struct oxi_batch_column {
+  const float* src;
+  float* dst;
+  int64_t inner;
+} oxi_batch_column;
+int oxi_batch_gather(const oxi_batch_column* cols, int ncols, int64_t len, const int64_t* idx, int64_t n);
 /* F.embedding (functional.py:245-247) = index_select on dim 0 of W (V, D). */
 int oxi_embedding_fwd(const float* W, const int64_t* ids, int64_t n,
                       int64_t V, int64_t D, float* out);

@@ -90,6 +90,7 @@ _SIGS = {
     "oxi_cross_entropy_fwd": [vp, vp, vp, vp, c_i64, c_i64],
     "oxi_cross_entropy_bwd": [vp, vp, vp, vp, vp, c_i64, c_i64],
     "oxi_index_select": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
+    "oxi_batch_gather": [vp, c_int, c_i64, vp, c_i64],
     "oxi_index_select_bwd": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
     "oxi_index_select_bwd_plan": [vp, c_i64, c_i64, ctypes.POINTER(vp)],
     "oxi_index_select_bwd_apply": [vp, vp, c_i64, c_i64, vp],
@@ -507,6 +508,24 @@ def masked_select_bwd(record: DeviceArray, x_shape, mask_shape, g: DeviceArray) 
     call("oxi_masked_select_bwd", record.ptr, _i64arr(grid), len(grid), g.ptr, g.size, gx.ptr,
          _i64arr(broadcast_elem_strides(tuple(x_shape), grid)), gx.size)
     return gx
+
+
+class BatchColumn(ctypes.Structure):
+    """oxi_batch_column"""
+    _fields_ = [("src", vp), ("dst", vp), ("inner", c_i64)]
+
+
+def batch_gather(columns, idx: DeviceArray, n: int | None = None) -> list:
+    """gather_columns: the rows `idx` of every (len, ...) column, one launch
+    per 8 columns; returns the new (n, ...) device arrays."""
+    n = idx.size if n is None else n
+    length = columns[0].shape[0] if columns else 0
+    outs = [DeviceArray((n,) + tuple(c.shape[1:])) for c in columns]
+    arr = (BatchColumn * max(1, len(columns)))()
+    for k, (c, o) in enumerate(zip(columns, outs)):
+        arr[k] = BatchColumn(c.ptr, o.ptr, int(np.prod(c.shape[1:], dtype=np.int64)))
+    call("oxi_batch_gather", ctypes.cast(arr, vp), len(columns), length, idx.ptr, n)
+    return outs
 
 
 class SgdSlice(ctypes.Structure):

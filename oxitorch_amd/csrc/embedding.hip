@@ -106,6 +106,82 @@ __global__ __launch_bounds__(BS) void gather_elem_k(const float* __restrict__ sr
 }
 
 // ---------------------------------------------------------------------------
+// Batch gather: the rows `idx` of up to BG_MAX columns sharing dim 0, one
+// launch. A block belongs to one column: GRPB rows of it (rows of 64 or more
+// floats, float4 when aligned) or BS elements (shorter rows).
+
+constexpr int BG_MAX = 8;
+enum BgMode : int { BG_ROWS = 0, BG_ROWS4 = 1, BG_ELEMS = 2 };
+
+struct BatchArgs {
+  const float* src[BG_MAX];
+  float* dst[BG_MAX];
+  int64_t inner[BG_MAX];
+  unsigned block_end[BG_MAX];  // exclusive end of each column's blocks
+  int mode[BG_MAX];
+  int count;
+};
+
+template <bool NTS>
+__global__ __launch_bounds__(BS) void batch_gather_k(BatchArgs a, int64_t len, const int64_t* __restrict__ idx,
+                                                     int64_t n, int* __restrict__ guard) {
+  int c = 0;
+  while (c + 1 < a.count && blockIdx.x >= a.block_end[c]) ++c;
+  const int64_t b = (int64_t)blockIdx.x - (c ? a.block_end[c - 1] : 0u);
+  const float* __restrict__ src = a.src[c];
+  float* __restrict__ dst = a.dst[c];
+  const int64_t inner = a.inner[c];
+  const int mode = a.mode[c];
+  if (mode == BG_ELEMS) {
+    const int64_t e = b * BS + threadIdx.x;
+    if (e < n * inner) {
+      const int64_t k = e / inner, i = e % inner;
+      bool ok;
+      const int64_t id = wrap_id(idx[k], len, ok);
+      if (!ok) atomicOr(guard, 1);
+      dst[e] = ok ? src[id * inner + i] : 0.f;
+    }
+    return;
+  }
+  const int64_t r0 = b * GRPB;
+  int64_t srow[GRPB];
+  bool okr[GRPB];
+#pragma unroll
+  for (int r = 0; r < GRPB; ++r) {
+    okr[r] = false;
+    srow[r] = 0;
+    if (r0 + r < n) {
+      bool ok;
+      const int64_t id = wrap_id(idx[r0 + r], len, ok);
+      okr[r] = ok;
+      srow[r] = id * inner;
+      if (!ok && threadIdx.x == 0) atomicOr(guard, 1);
+    }
+  }
+  if (mode == BG_ROWS4) {
+    const int64_t units = inner / 4;
+    for (int64_t u = threadIdx.x; u < units; u += BS) {
+      f4 v[GRPB];
+#pragma unroll
+      for (int r = 0; r < GRPB; ++r)
+        v[r] = (r0 + r < n && okr[r]) ? reinterpret_cast<const f4*>(src + srow[r])[u] : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < GRPB; ++r)
+        if (r0 + r < n) st_stream<NTS>(v[r], reinterpret_cast<f4*>(dst + (r0 + r) * inner) + u);
+    }
+  } else {
+    for (int64_t u = threadIdx.x; u < inner; u += BS) {
+      float v[GRPB];
+#pragma unroll
+      for (int r = 0; r < GRPB; ++r) v[r] = (r0 + r < n && okr[r]) ? src[srow[r] + u] : 0.f;
+#pragma unroll
+      for (int r = 0; r < GRPB; ++r)
+        if (r0 + r < n) dst[(r0 + r) * inner + u] = v[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // VJP, sort: stable LSD radix sort of (key, position) pairs, 8-bit digits.
 // Keys are the ids wrapped to [0, len); an out-of-range id gets the sentinel
 // key `len` (sorted last, never summed) and raises the guard flag. A block owns
@@ -741,6 +817,58 @@ int oxi_index_select(const float* src, int64_t outer, int64_t len, int64_t inner
     gather_elem_k<<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(src, outer, len, inner, idx, n, out, guard_flag());
   }
   return check_launch("index_select");
+}
+
+int oxi_batch_gather(const oxi_batch_column* cols, int ncols, int64_t len, const int64_t* idx, int64_t n) {
+  if (ncols < 0 || n < 0 || len < 0) return fail(OXI_INVALID_ARGUMENT, "batch_gather: negative size");
+  if (ncols > 0 && !cols) return fail(OXI_INVALID_ARGUMENT, "batch_gather: NULL column list");
+  int64_t out_bytes = 0;
+  for (int c = 0; c < ncols; ++c) {
+    const oxi_batch_column& col = cols[c];
+    if (col.inner < 0) return fail(OXI_INVALID_ARGUMENT, "batch_gather: column %d has a negative row size", c);
+    if (int rc = check_sizes("batch_gather", 1, len, col.inner, n)) return rc;
+    if (n > 0 && col.inner > 0 && (!col.src || !col.dst))
+      return fail(OXI_INVALID_ARGUMENT, "batch_gather: column %d has a NULL pointer", c);
+    out_bytes += n * col.inner * 4;
+  }
+  if (out_bytes == 0) return OXI_OK;
+  if (len == 0) return fail(OXI_OUT_OF_BOUNDS, "batch_gather: indices into an empty dataset");
+  if (!idx) return fail(OXI_INVALID_ARGUMENT, "batch_gather: NULL indices");
+  OXI_CHECK_INIT();
+  hipStream_t s = stream();
+  const bool nts = nt_stores(out_bytes);
+  BatchArgs a{};
+  int64_t blocks = 0;
+  auto flush = [&]() -> int {
+    if (a.count == 0) return OXI_OK;
+    if (nts) batch_gather_k<true><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(a, len, idx, n, guard_flag());
+    else batch_gather_k<false><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(a, len, idx, n, guard_flag());
+    a = BatchArgs{};
+    blocks = 0;
+    return check_launch("batch_gather");
+  };
+  for (int c = 0; c < ncols; ++c) {
+    const oxi_batch_column& col = cols[c];
+    if (col.inner == 0) continue;
+    int mode = BG_ELEMS;
+    int64_t nb = ceil_div(n * col.inner, BS);
+    if (col.inner >= 64) {
+      mode = (col.inner % 4 == 0 && al16(col.src) && al16(col.dst)) ? BG_ROWS4 : BG_ROWS;
+      nb = ceil_div(n, GRPB);
+    }
+    if (a.count == BG_MAX || blocks + nb >= ((int64_t)1 << 31)) {
+      if (int rc = flush()) return rc;
+    }
+    if (nb >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "batch_gather: column %d is too large", c);
+    a.src[a.count] = col.src;
+    a.dst[a.count] = col.dst;
+    a.inner[a.count] = col.inner;
+    a.mode[a.count] = mode;
+    blocks += nb;
+    a.block_end[a.count] = (unsigned)blocks;
+    ++a.count;
+  }
+  return flush();
 }
 
 int oxi_index_select_bwd_plan(const int64_t* idx, int64_t n, int64_t len, void** plan) {

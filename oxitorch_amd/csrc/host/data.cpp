@@ -1,9 +1,10 @@
 // The tensor-column loader of the host core (crates/oxi-data/src/{batch,rng}.rs,
 // crates/oxi-bindings/src/data.rs): the dataset's columns live in HBM for the
 // loader's lifetime, each epoch's row order is uploaded once, and a batch is
-// one device gather per column at an offset into that order. No batch
-// crosses PCIe; the only host work, the next epoch's shuffled order, runs on
-// a host thread while the current epoch is consumed.
+// one device gather of all columns at an offset into that order. No batch
+// crosses PCIe; the only host work, the shuffled orders of the coming epochs,
+// runs on host threads (num_workers of them, at least one) while the current
+// epoch is consumed.
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -20,13 +21,22 @@ Mt19937::Mt19937(uint32_t seed) {
   mti_ = 624;
 }
 
+namespace {
+// One word of the twist: the top bit of `cur`, the low 31 of `nxt`, mixed
+// into the word 397 places on (branch-free form of the twist matrix).
+inline uint32_t twist_word(uint32_t cur, uint32_t nxt, uint32_t far) {
+  const uint32_t y = (cur & 0x80000000u) | (nxt & 0x7fffffffu);
+  return far ^ (y >> 1) ^ (0x9908b0dfu & (0u - (y & 1u)));
+}
+}  // namespace
+
+// In place, in index order: words past 623-397 read already-twisted words,
+// as the generator defines.
 void Mt19937::twist() {
-  for (int i = 0; i < 624; ++i) {
-    const uint32_t y = (mt_[i] & 0x80000000u) | (mt_[(i + 1) % 624] & 0x7fffffffu);
-    uint32_t next = mt_[(i + 397) % 624] ^ (y >> 1);
-    if (y & 1u) next ^= 0x9908b0dfu;
-    mt_[i] = next;
-  }
+  int i = 0;
+  for (; i < 624 - 397; ++i) mt_[i] = twist_word(mt_[i], mt_[i + 1], mt_[i + 397]);
+  for (; i < 623; ++i) mt_[i] = twist_word(mt_[i], mt_[i + 1], mt_[i + 397 - 624]);
+  mt_[623] = twist_word(mt_[623], mt_[0], mt_[396]);
   mti_ = 0;
 }
 
@@ -97,18 +107,25 @@ Loader::Loader(const std::vector<Tensor>& columns, int64_t batch_size, bool shuf
   for (const Tensor& c : columns) columns_.push_back(t_contiguous(c.dev() == Dev::Hip ? c : t_to(c, Dev::Hip)));
 }
 
-void Loader::prefetch_order() {
-  // EpochSeeds::next (data.rs:40-48): base + epoch, truncated to 32 bits
-  const uint32_t seed = (uint32_t)(*seed_ + epoch_++);
-  const int64_t n = n_;
-  pending_ = std::async(std::launch::async, [seed, n]() { return Mt19937(seed).permutation(n); });
+// Keeps the orders of the next epochs in flight on host threads: each
+// epoch's seed is fixed in advance, so they are independent. `num_workers`
+// (the reference's host thread count) sets how many, at least one.
+void Loader::prefetch_orders() {
+  const size_t depth = (size_t)std::max<int64_t>(1, workers_);
+  while (pending_.size() < depth) {
+    // EpochSeeds::next (data.rs:40-48): base + epoch, truncated to 32 bits
+    const uint32_t seed = (uint32_t)(*seed_ + epoch_++);
+    const int64_t n = n_;
+    pending_.push_back(std::async(std::launch::async, [seed, n]() { return Mt19937(seed).permutation(n); }));
+  }
 }
 
 std::vector<int64_t> Loader::next_order() {
   if (shuffle_ && seed_) {
-    if (!pending_.valid()) prefetch_order();
-    std::vector<int64_t> order = pending_.get();
-    prefetch_order();
+    prefetch_orders();
+    std::vector<int64_t> order = pending_.front().get();
+    pending_.pop_front();
+    prefetch_orders();
     return order;
   }
   std::vector<int64_t> order((size_t)n_);
@@ -129,16 +146,19 @@ bool LoaderIter::next(std::vector<Tensor>* out) {
   const auto [start, len] = batches[pos++];
   const int64_t* ids = static_cast<const int64_t*>(order->ptr) + start;
   out->clear();
+  // every column of the batch in one launch (gather_columns, batch.rs:406-423)
+  std::vector<oxi_batch_column> cols;
+  cols.reserve(columns.size());
   for (const Tensor& c : columns) {
     Shape shape = c.shape;
-    const int64_t rows = shape[0];
     shape[0] = len;
     int64_t inner = 1;
     for (size_t d = 1; d < shape.size(); ++d) inner *= shape[d];
     Tensor b = Tensor::empty(shape, Dev::Hip);
-    if (b.numel() > 0) hip_check(oxi_index_select(c.data(), 1, rows, inner, ids, len, b.data()));
+    if (b.numel() > 0) cols.push_back({c.data(), b.data(), inner});
     out->push_back(std::move(b));
   }
+  if (!cols.empty()) hip_check(oxi_batch_gather(cols.data(), (int)cols.size(), columns[0].shape[0], ids, len));
   return true;
 }
 

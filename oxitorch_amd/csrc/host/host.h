@@ -9,6 +9,7 @@
 #pragma once
 
 #include <cstdint>
+#include <deque>
 #include <functional>
 #include <future>
 #include <memory>
@@ -305,11 +306,11 @@ class Loader {
 
  private:
   std::vector<int64_t> next_order();
-  void prefetch_order();
+  void prefetch_orders();
   std::vector<Tensor> columns_;  // contiguous, device-resident
-  // the next shuffled epoch's order, computed on a host thread while the
+  // the next shuffled epochs' orders, computed on host threads while the
   // current epoch runs (the permutation is the loader's only host work)
-  std::future<std::vector<int64_t>> pending_;
+  std::deque<std::future<std::vector<int64_t>>> pending_;
   int64_t n_ = 0, batch_size_ = 1;
   bool shuffle_ = false, drop_last_ = false;
   std::optional<uint64_t> seed_;

@@ -6,9 +6,10 @@ Same API as the reference module. Two paths behind one `DataLoader`:
   dim 0, e.g. `TensorDataset`) with the default collation and no custom
   sampler: `_native.DataLoader` keeps the columns in HBM for the loader's
   lifetime, uploads each epoch's row order once, and gathers every batch on
-  the device, one launch per column. Shuffled orders are NumPy's
+  the device, one launch for all columns. Shuffled orders are NumPy's
   `RandomState(seed + epoch).permutation(n)`, as in the reference's native
-  loader. `num_workers` is accepted; no host threads are needed.
+  loader. The only host work is each epoch's permutation; `num_workers`
+  host threads (at least one) compute the coming epochs' orders ahead.
 - **Generic path** for any other `Dataset` / `IterableDataset`: items are
   fetched per index (through a thread pool when `num_workers > 1`) and
   collated with `default_collate`; the collated batch is uploaded through the

@@ -16,6 +16,13 @@ from conftest import rng
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(scope="module")
+def oracle():
+    from oracle import ref
+
+    return ref
+
+
 def say(*a):
     print("[case]", *a, flush=True)
     sys.stdout.flush()
@@ -86,19 +93,22 @@ def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("n,bs,drop", [(1000, 64, False), (1000, 64, True), (257, 300, True), (4096, 1024, False)])
-def test_device_loader_matches_numpy_gather(ox, n, bs, drop):
-    """Three epochs: each batch of each column equals the NumPy gather of the
-    epoch's RandomState(seed + epoch) order, bit for bit."""
+@pytest.mark.parametrize("n,bs,drop,workers", [(1000, 64, False, 0), (1000, 64, True, 0), (257, 300, True, 0),
+                                               (4096, 1024, False, 0), (1000, 64, False, 3), (4096, 1024, True, 8)])
+def test_device_loader_matches_numpy_gather(ox, n, bs, drop, workers):
+    """Five epochs: each batch of each column equals the NumPy gather of the
+    epoch's RandomState(seed + epoch) order, bit for bit, however many epochs'
+    orders the host threads compute ahead."""
     from oxitorch_amd import _native
 
-    say("device loader", n, bs, drop)
+    say("device loader", n, bs, drop, workers)
     r = rng(n + bs)
     x = r.standard_normal((n, 3, 4), dtype=np.float32)
     y = np.arange(n, dtype=np.float32)
-    loader = _native.DataLoader([_t(ox, x), _t(ox, y)], batch_size=bs, shuffle=True, drop_last=drop, seed=1234)
+    loader = _native.DataLoader([_t(ox, x), _t(ox, y)], batch_size=bs, shuffle=True, drop_last=drop, seed=1234,
+                                num_workers=workers)
     assert loader.n == n and loader.batch_size == bs
-    for epoch in range(3):
+    for epoch in range(5):
         order = np.random.RandomState(1234 + epoch).permutation(n)
         plan = _native._epoch_plan(n, bs, drop)
         got = list(iter(loader))
@@ -108,6 +118,35 @@ def test_device_loader_matches_numpy_gather(ox, n, bs, drop):
             assert np.array_equal(_bits(bx.numpy()), _bits(x[rows]))
             assert np.array_equal(_bits(by.numpy()), _bits(y[rows]))
             assert not bx.requires_grad and bx.device.startswith("hip")
+
+
+def test_batch_gather_all_column_kinds(hip, oracle):
+    """One launch per 8 columns: float4 rows, unaligned scalar rows, short
+    rows and 1-D columns, 11 columns in all; negative ids wrap; every column
+    equals the oracle's index_select bit for bit."""
+    say("batch_gather")
+    r = rng(91)
+    n_rows = 3001
+    shapes = [(n_rows, 784), (n_rows,), (n_rows, 66), (n_rows, 3, 4), (n_rows, 64), (n_rows, 1), (n_rows, 130),
+              (n_rows, 7), (n_rows, 256), (n_rows,), (n_rows, 2, 40)]
+    cols = [r.standard_normal(sh, dtype=np.float32) for sh in shapes]
+    ids = r.integers(-n_rows, n_rows, 1000).astype(np.int64)
+    d_cols = [hip.DeviceArray.from_numpy(c) for c in cols]
+    outs = hip.batch_gather(d_cols, hip.DeviceArray.from_numpy(ids))
+    hip.sync()
+    for c, o in zip(cols, outs):
+        want = oracle.index_select(c.reshape(n_rows, -1), 0, ids).reshape((len(ids),) + c.shape[1:])
+        assert np.array_equal(_bits(o.numpy()), _bits(want)), c.shape
+    # an out-of-range id writes zeros and raises the guard
+    bad = ids.copy()
+    bad[5] = n_rows
+    outs = hip.batch_gather(d_cols[:2], hip.DeviceArray.from_numpy(bad))
+    with pytest.raises(RuntimeError, match="guard|out of range|index"):
+        hip.sync()
+    hip.sync()
+    assert not outs[0].numpy()[5].any() and outs[1].numpy()[5] == 0.0
+    with pytest.raises(ValueError, match="NULL"):
+        hip.call("oxi_batch_gather", None, 2, n_rows, None, 4)
 
 
 def test_device_loader_sequential_and_unseeded_shuffle(ox):
