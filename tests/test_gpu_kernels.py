@@ -366,6 +366,37 @@ def test_index_select_bwd_run_shapes(hip, case):
     assert_reduction_close(got, want32, exact, what=f"index_select_bwd {case}")
 
 
+@pytest.mark.parametrize("n,V", [(16384, 50257), (16385, 50257), (1, 7), (3000, 65535), (3000, 65536),
+                                 (12000, 16), (9000, 300)])
+def test_index_select_bwd_sort_limits(hip, n, V):
+    """Sizes around the sort's tile and table limits (16384 ids, tables of
+    65535 and 65536 rows, 1 to 3 radix passes): Zipf ids with negatives
+    and repeats; rows whose runs sit in one segment tile are bit-exact with
+    the oracle's position-order sums, the rest within the reduction bar of
+    float64; absent keys are zero; two calls agree bitwise."""
+    from oracle import ref
+    say("index_select_bwd sort limits", n, V)
+    r = rng(n + V)
+    ids = np.minimum(r.zipf(1.2, n) - 1, V - 1).astype(np.int64)
+    neg = r.random(n) < 0.1
+    ids[neg] -= V  # same rows, written as negatives
+    Dm = 8
+    g = r.standard_normal((n, Dm), dtype=np.float32)
+    dg, di = D(hip, g), D(hip, ids)
+    got = hip.index_select_bwd(dg, (V, Dm), 0, di).numpy()
+    again = hip.index_select_bwd(dg, (V, Dm), 0, di).numpy()
+    hip.sync()
+    np.testing.assert_array_equal(got, again)
+    keys = np.where(ids < 0, ids + V, ids)
+    want32 = ref.index_select_bwd(g, (V, Dm), 0, ids)
+    exact = _exact_bwd(g, (V, Dm), 0, ids)
+    one = segmented_runs_in_one_tile(keys, V)
+    np.testing.assert_array_equal(got[one], want32[one])
+    absent = np.bincount(keys, minlength=V) == 0
+    np.testing.assert_array_equal(got[absent], 0.0)
+    assert_reduction_close(got, want32, exact, what=f"index_select_bwd n={n} V={V}")
+
+
 @pytest.mark.parametrize("case", ["skewed_outer", "zipf_vocab", "empty"])
 def test_index_select_bwd_plan_matches_one_call(hip, case):
     """The sort plan queued on the second stream, applied (twice, as a second
