@@ -106,6 +106,27 @@ __device__ __forceinline__ T group_sum(T v, T* lds) {
   return v;
 }
 
+// group_sum / group_max without the leading barrier, which only keeps a
+// reduction from overwriting slots that waves still read from the one
+// before. Callers give consecutive reductions alternate slot sets (`lds`
+// holds TPR/64 values each): every wave reads a reduction's slots before it
+// reaches the next reduction's barrier, so a set is free again by the
+// reduction after that. The first reduction of a kernel may take either set.
+template <int TPR, typename T>
+__device__ __forceinline__ T group_sum_once(T v, T* lds) {
+  v = wave_sum(v);
+  if constexpr (TPR > 64) {
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    v = lds[0];
+#pragma unroll
+    for (int i = 1; i < TPR / 64; ++i) v += lds[i];
+  }
+  return v;
+}
+
 template <int TPR>
 __device__ __forceinline__ float group_max(float v, float* lds) {
   v = wave_max(v);
@@ -113,6 +134,21 @@ __device__ __forceinline__ float group_max(float v, float* lds) {
     const int lane = threadIdx.x & 63;
     const int wid = threadIdx.x >> 6;
     __syncthreads();
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    v = lds[0];
+#pragma unroll
+    for (int i = 1; i < TPR / 64; ++i) v = fmaxf(v, lds[i]);
+  }
+  return v;
+}
+
+template <int TPR>
+__device__ __forceinline__ float group_max_once(float v, float* lds) {
+  v = wave_max(v);
+  if constexpr (TPR > 64) {
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
     if (lane == 0) lds[wid] = v;
     __syncthreads();
     v = lds[0];

@@ -26,6 +26,9 @@ constexpr int BS = 256;
 
 template <int TPR>
 __device__ __forceinline__ float rsum(float v, float* lds) { return group_sum<TPR, float>(v, lds); }
+// one barrier per reduction; consecutive reductions alternate slot sets
+template <int TPR>
+__device__ __forceinline__ float rsum1(float v, float* lds) { return group_sum_once<TPR, float>(v, lds); }
 
 // ---------------------------------------------------------------------------
 // Forward, register-resident rows.
@@ -37,7 +40,7 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void norm_fwd_k(const flo
                                                  int64_t rows, int H, float eps) {
   constexpr int NT = row_block_threads(TPR);
   constexpr int GPB = NT / TPR;
-  __shared__ float lds[NT / 64];
+  __shared__ float lds[2 * (NT / 64)];  // mean, then variance
   const int t = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * GPB + threadIdx.x / TPR;
   if (row >= rows) return;  // GPB == 1 whenever TPR > 64: the whole block leaves together
@@ -50,7 +53,7 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void norm_fwd_k(const flo
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) s += (xt.v[k].x + xt.v[k].y) + (xt.v[k].z + xt.v[k].w);
-    mu = rsum<TPR>(s, lds) / fH;
+    mu = rsum1<TPR>(s, lds) / fH;
 #pragma unroll
     for (int k = 0; k < NV; ++k)
       if (k * TPR + t < h4) xt.v[k] = xt.v[k] - mu;  // centered; padding stays 0
@@ -61,7 +64,7 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void norm_fwd_k(const flo
     const f4 v = xt.v[k];
     ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
   }
-  const float var = rsum<TPR>(ss, lds) / fH;
+  const float var = rsum1<TPR>(ss, lds + NT / 64) / fH;
   const float inv = 1.0f / sqrtf(var + eps);
   if (t == 0) {
     if (rstd) rstd[row] = inv;
@@ -161,6 +164,8 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
   // flight while the current row is reduced and stored
   const int64_t ngroups = (int64_t)gridDim.x * GPB;
   int64_t row = (int64_t)blockIdx.x * GPB + gi;
+  int red = 0;  // reductions so far: consecutive ones use alternate LDS slot sets
+  auto slot = [&]() { return lds + ((red++ & 1) ? BS / 64 : 0); };
   RowTile<TPR, NV> xt, gt;
   float inv = 0.f, mu = 0.f;
   if (row < rows) {
@@ -199,7 +204,7 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
           s += (gt.v[k].x + gt.v[k].y) + (gt.v[k].z + gt.v[k].w);
         }
         if constexpr (LN) {
-          const float corr = (-rsum<TPR>(s, lds)) * inv_n;
+          const float corr = (-rsum1<TPR>(s, slot())) * inv_n;
 #pragma unroll
           for (int k = 0; k < NV; ++k) gt.v[k] = gt.v[k] + corr;
         }
@@ -214,8 +219,8 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
           sa += (gt.v[k].x + gt.v[k].y) + (gt.v[k].z + gt.v[k].w);
         }
         float a = 0.f;
-        if constexpr (LN) a = rsum<TPR>(sa, lds) * inv_n;
-        const float bcoef = rsum<TPR>(sb, lds + BS / 64) * inv_n;
+        if constexpr (LN) a = rsum1<TPR>(sa, slot()) * inv_n;
+        const float bcoef = rsum1<TPR>(sb, slot()) * inv_n;
 #pragma unroll
         for (int k = 0; k < NV; ++k) gt.v[k] = ((gt.v[k] - a) - xt.v[k] * bcoef) * inv;
       }
@@ -377,9 +382,7 @@ void launch_fwd_cfg(int cfg, hipStream_t s, const float* x, const float* w, cons
 #define OXI_FWD(TPR, NV)                                                                                   \
   case TPR * 10 + NV:                                                                                      \
     norm_fwd_k<TPR, NV, LN, NTS><<<dim3((unsigned)ceil_div(rows, row_block_threads(TPR) / TPR)),          \
-                                   dim3(row_block_threads(TPR)), 0, s>>>(x, w, b, y,                         \
-                                                                                             mean, rstd,   \
-                                                                                             rows, h, eps); \
+                                   dim3(row_block_threads(TPR)), 0, s>>>(x, w, b, y, mean, rstd, rows, h, eps); \
     break;
   switch (cfg) {
     OXI_FWD(64, 1)

@@ -82,7 +82,7 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void sm_fwd_k(const float
 #pragma unroll
   for (int k = 0; k < NV; ++k)
     if (k * TPR + t < h4) m = fmaxf(m, max4(xt.v[k]));
-  m = group_max<TPR>(m, lds);
+  m = group_max_once<TPR>(m, lds);  // one row per block: one barrier per reduction
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -93,7 +93,7 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void sm_fwd_k(const float
       xt.v[k] = LOG ? z : e;
     }
   }
-  s = group_sum<TPR, float>(s, lds + NT / 64);
+  s = group_sum_once<TPR, float>(s, lds + NT / 64);
   if constexpr (LOG) {
     const float L = logf(s);
 #pragma unroll
@@ -121,7 +121,7 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void sm_bwd_k(const float
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) s += LOG ? sum4(gt.v[k]) : sum4(gt.v[k] * yt.v[k]);
-  s = group_sum<TPR, float>(s, lds);
+  s = group_sum_once<TPR, float>(s, lds);  // the block's only reduction
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     if constexpr (LOG) gt.v[k] = gt.v[k] - exp4(yt.v[k]) * s;
