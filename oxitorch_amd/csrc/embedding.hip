@@ -927,6 +927,9 @@ int oxi_index_select_bwd_plan_free(void* plan) {
   // reused, and before its events go back to the pool
   if (p->recorded && ensure_init() && hipEventQuery(p->ready) != hipSuccess)
     (void)hipStreamWaitEvent(stream(), p->ready, 0);
+  // a plan whose build failed part-way has no completion event: kernels it
+  // queued may still run on the side stream, so drain it (error path only)
+  if (!p->recorded && p->ws) (void)hipStreamSynchronize(side_stream());
   if (p->ws) ws_free(p->ws);
   give_event(p->queued);
   give_event(p->ready);
