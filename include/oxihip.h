@@ -150,6 +150,9 @@ int oxi_hip_debug_fail_alloc_after(int n);
 
 /* ------------------------------------------------------------------------ */
 /* Elementwise registry on strided/broadcast operands.                      */
+/* Strides are in elements, one per dim of `shape` (0 for a broadcast dim);  */
+/* with ndim == 0 (a single element) `shape` and the stride arrays may be    */
+/* NULL.                                                                     */
 
 /* y = fill value (n contiguous floats). Used for Tensor::zeros/full
  * (lib.rs:67-158) and the scalar-operand promotion of const_full

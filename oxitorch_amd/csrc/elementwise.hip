@@ -334,6 +334,7 @@ template <int N>
 int build_plan(Plan<N>& p, float* y, const int64_t* ys, const float* const* xs, const int64_t* const* xst,
                const int64_t* shape, int ndim, int64_t* numel) {
   if (ndim < 0 || ndim > MAXD) return fail(OXI_INVALID_ARGUMENT, "rank %d exceeds the supported %d dims", ndim, MAXD);
+  if (ndim > 0 && !shape) return fail(OXI_INVALID_ARGUMENT, "NULL shape");
   int64_t n = 1;
   for (int d = 0; d < ndim; ++d) {
     if (shape[d] < 0) return fail(OXI_INVALID_ARGUMENT, "negative dim size %lld", (long long)shape[d]);
@@ -349,6 +350,12 @@ int build_plan(Plan<N>& p, float* y, const int64_t* ys, const float* const* xs, 
   if (!y) return fail(OXI_INVALID_ARGUMENT, "NULL output pointer");
   for (int k = 0; k < N; ++k)
     if (!xs[k]) return fail(OXI_INVALID_ARGUMENT, "NULL input pointer");
+  // a 0-d operand has no strides: its stride arrays may be NULL
+  if (ndim > 0) {
+    if (!ys) return fail(OXI_INVALID_ARGUMENT, "NULL output strides");
+    for (int k = 0; k < N; ++k)
+      if (!xst[k]) return fail(OXI_INVALID_ARGUMENT, "NULL input strides");
+  }
   // collect non-trivial dims
   struct Dim { int64_t size; int64_t st[N + 1]; };
   Dim dims[MAXD];
@@ -356,11 +363,10 @@ int build_plan(Plan<N>& p, float* y, const int64_t* ys, const float* const* xs, 
   for (int d = 0; d < ndim; ++d) {
     if (shape[d] == 1) continue;
     dims[m].size = shape[d];
-    dims[m].st[0] = ys ? ys[d] : 0;
-    for (int k = 0; k < N; ++k) dims[m].st[k + 1] = xst[k] ? xst[k][d] : 0;
+    dims[m].st[0] = ys[d];
+    for (int k = 0; k < N; ++k) dims[m].st[k + 1] = xst[k][d];
     ++m;
   }
-  if (!ys) return fail(OXI_INVALID_ARGUMENT, "NULL output strides");
   // order dims by decreasing |output stride| (stable): iteration follows the
   // output's memory order, so a row-major output is walked row-major.
   std::stable_sort(dims, dims + m, [](const Dim& a, const Dim& b) {

@@ -366,6 +366,26 @@ def test_index_select_bwd_run_shapes(hip, case):
     assert_reduction_close(got, want32, exact, what=f"index_select_bwd {case}")
 
 
+def test_elementwise_zero_d_operands(hip):
+    """A 0-d operand has no strides: with ndim 0, NULL shape and stride arrays
+    are accepted; NULL strides with ndim > 0 are refused before any launch."""
+    say("elementwise 0-d")
+    a, b = D(hip, np.array([3.0], np.float32)), D(hip, np.array([2.0], np.float32))
+    y = hip.DeviceArray((1,))
+    mul = hip.BINARY.index("mul")
+    hip.call("oxi_binary", mul, a.ptr, None, b.ptr, None, y.ptr, None, None, 0)
+    assert y.numpy().tolist() == [6.0]
+    hip.call("oxi_unary", hip.UNARY.index("neg"), a.ptr, None, y.ptr, None, None, 0)
+    assert y.numpy().tolist() == [-3.0]
+    # operands sized for the shape, so that even a launch would stay in bounds
+    a2, b2, y2 = D(hip, np.ones(2, np.float32)), D(hip, np.ones(2, np.float32)), hip.DeviceArray((2,))
+    one, two = hip._i64arr([1]), hip._i64arr([2])
+    with pytest.raises(ValueError, match="NULL input strides"):
+        hip.call("oxi_binary", mul, a2.ptr, None, b2.ptr, one, y2.ptr, one, two, 1)
+    with pytest.raises(ValueError, match="NULL output strides"):
+        hip.call("oxi_binary", mul, a2.ptr, one, b2.ptr, one, y2.ptr, None, two, 1)
+
+
 @pytest.mark.parametrize("n,V", [(16384, 50257), (16385, 50257), (1, 7), (3000, 65535), (3000, 65536),
                                  (12000, 16), (9000, 300)])
 def test_index_select_bwd_sort_limits(hip, n, V):
