@@ -1,0 +1,176 @@
+"""The reference autograd crate's gradchecks (crates/oxi-autograd/src/tests.rs,
+harness crates/oxi-autograd/src/gradcheck.rs:15-80), restated on the device:
+every analytic VJP is compared with central differences of `w · f(x)`
+evaluated in float32 (h = 1e-2, tolerance 1e-3 · max(1, |analytic|)), on the
+reference's own pseudo-random inputs (its xorshift `rng_vec`, tests.rs:83-95).
+Matrix products (SGEMM is outside this build) are left out."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+H = np.float32(1e-2)
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def ox(hip):
+    import oxitorch_amd
+
+    return oxitorch_amd
+
+
+def rng_vec(n, seed):
+    """tests.rs:83-95: xorshift64 draws mapped to (state % 2000) / 1000 - 1 in f32."""
+    mask = (1 << 64) - 1
+    state = (seed | 1) & mask
+    out = np.empty(n, np.float32)
+    for i in range(n):
+        state ^= (state << 13) & mask
+        state ^= state >> 7
+        state ^= (state << 17) & mask
+        out[i] = np.float32(state % 2000) / np.float32(1000.0) - np.float32(1.0)
+    return out
+
+
+def _t(ox, a, requires_grad=False):
+    return ox.from_numpy(np.ascontiguousarray(a, dtype=np.float32), requires_grad)
+
+
+def _to_scalar(t):
+    while len(t.shape) > 0:
+        t = t.sum(0)
+    return t
+
+
+def _weighted(ox, out, w):
+    return _to_scalar(out * _t(ox, w))
+
+
+def check_with_weights(ox, x, w, f, tol=TOL):
+    """gradcheck.rs:66-80: loss = sum(f(x) * w); analytic grad vs central differences."""
+    xv = _t(ox, x, True)
+    _weighted(ox, f(xv), w).backward()
+    analytic = xv.grad.numpy().ravel()
+    base = np.asarray(x, np.float32).ravel()
+    with ox.no_grad():
+        for i in range(base.size):
+            plus, minus = base.copy(), base.copy()
+            plus[i] += H
+            minus[i] -= H
+            fp = float(_weighted(ox, f(_t(ox, plus.reshape(np.shape(x)))), w))
+            fm = float(_weighted(ox, f(_t(ox, minus.reshape(np.shape(x)))), w))
+            numeric = np.float32(np.float32(fp) - np.float32(fm)) / (np.float32(2.0) * H)
+            assert abs(analytic[i] - numeric) <= tol * max(abs(analytic[i]), 1.0), (i, analytic[i], numeric)
+    return True
+
+
+def check_scalar(ox, x, f, tol=TOL):
+    """gradcheck.rs:24-60: f returns a scalar."""
+    return check_with_weights(ox, x, np.float32(1.0), f, tol)
+
+
+def test_add_sub_mul_div_pow_gradcheck(ox):
+    a = rng_vec(6, 1).reshape(2, 3)
+    b = rng_vec(6, 2).reshape(2, 3)
+    w = rng_vec(6, 3).reshape(2, 3)
+    bb = rng_vec(3, 4)
+    check_with_weights(ox, a, w, lambda x: x + _t(ox, b))
+    check_with_weights(ox, b, w, lambda y: _t(ox, a) + y)
+    check_with_weights(ox, bb, w, lambda y: _t(ox, a) + y)  # [3] broadcast over [2, 3]
+    check_with_weights(ox, a, w, lambda x: x - _t(ox, b))
+    check_with_weights(ox, a, w, lambda x: x * _t(ox, b))
+    # d(x / b)/dx = 1 / b is exact under central differences, whatever b's size
+    check_with_weights(ox, a, w, lambda x: x / _t(ox, b))
+    pos = np.abs(a) + np.float32(0.5)
+    check_scalar(ox, pos, lambda x: (x * x).sum(0).sum(0))
+
+
+def test_unaries_gradcheck(ox):
+    a = (np.abs(rng_vec(6, 5)) + np.float32(0.5)).reshape(2, 3)
+    w = rng_vec(6, 6).reshape(2, 3)
+    for name in ["exp", "log", "sqrt", "tanh", "sigmoid", "neg"]:
+        check_with_weights(ox, a, w, lambda x, n=name: x.apply(n))
+    shifted = np.where(np.abs(a) < 0.2, a + np.float32(0.3), a).astype(np.float32)
+    check_with_weights(ox, shifted, w, lambda x: x.apply("relu"))
+
+
+def test_reductions_gradcheck(ox):
+    a = rng_vec(12, 9).reshape(3, 4)
+    check_with_weights(ox, a, rng_vec(3, 10).reshape(3, 1), lambda x: x.sum(1, keepdim=True))
+    check_with_weights(ox, a, rng_vec(4, 11).reshape(1, 4), lambda x: x.mean(0, keepdim=True))
+    check_with_weights(ox, a, rng_vec(3, 12).reshape(3, 1), lambda x: x.norm(1, keepdim=True))
+
+
+def test_views_gradcheck(ox):
+    a = rng_vec(12, 13).reshape(3, 4)
+    w43 = rng_vec(12, 17).reshape(4, 3)
+    w24 = rng_vec(8, 18).reshape(2, 4)
+    w34 = rng_vec(12, 14).reshape(3, 4)
+    check_with_weights(ox, a, w43, lambda x: x.transpose())
+    check_with_weights(ox, a, w43, lambda x: x.reshape([4, 3]))
+    check_with_weights(ox, a, w24, lambda x: x.narrow(0, 1, 3, 1))  # narrow_dim0(x, 1, 2)
+    check_with_weights(ox, a, w34, lambda x: x.broadcast_to([3, 4]))
+
+
+def test_permute_gradcheck_and_backward(ox):
+    arr = rng_vec(24, 19).reshape(2, 3, 4)
+    wgt = rng_vec(24, 20).reshape(4, 2, 3)
+    check_with_weights(ox, arr, wgt, lambda x: x.permute([2, 0, 1]))
+    x = _t(ox, rng_vec(24, 21).reshape(2, 3, 4), True)
+    y = x.permute([2, 0, 1]).permute([1, 2, 0])
+    assert np.array_equal(y.numpy(), x.numpy()) and tuple(y.shape) == tuple(x.shape)
+    _to_scalar(x.permute([2, 0, 1])).backward()
+    assert x.grad.numpy().ravel().tolist() == [1.0] * 24
+
+
+def test_scatter_dim0_gradcheck_and_last_write_wins(ox):
+    base = rng_vec(12, 20).reshape(4, 3)
+    vals = rng_vec(9, 21).reshape(3, 3)
+    w = rng_vec(12, 22).reshape(4, 3)
+    check_with_weights(ox, base, w, lambda b: b.scatter([1, 3, 1], _t(ox, vals)))
+    check_with_weights(ox, vals, w, lambda v: _t(ox, base).scatter([1, 3, 1], v))
+    b = _t(ox, [[10.0, 11.0], [20.0, 21.0], [30.0, 31.0]], True)
+    v = _t(ox, [[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], True)
+    out = b.scatter([2, 0, 2], v)
+    (out * _t(ox, np.ones((3, 2)))).sum(0).sum(0).backward()
+    assert b.grad.numpy().ravel().tolist() == [0.0, 0.0, 1.0, 1.0, 0.0, 0.0]
+    assert v.grad.numpy().ravel().tolist() == [0.0, 0.0, 1.0, 1.0, 1.0, 1.0]
+
+
+def test_masked_select_gradcheck_and_broadcast_accumulation(ox):
+    data = rng_vec(6, 25).reshape(2, 3)
+    mask = np.array([[1.0, 0.0, 1.0], [0.0, 1.0, 0.0]], np.float32)
+    check_with_weights(ox, data, np.array([1.0, 2.0, 3.0], np.float32), lambda x: x.masked_select(_t(ox, mask)))
+    x = _t(ox, [[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], True)
+    out = x.masked_select(_t(ox, [1.0, 0.0, 1.0]))
+    (out * _t(ox, [10.0, 20.0, 30.0, 40.0])).sum(0).backward()
+    assert x.grad.numpy().ravel().tolist() == [10.0, 0.0, 20.0, 30.0, 0.0, 40.0]
+    col = _t(ox, [[7.0], [9.0]], True)
+    outc = col.masked_select(_t(ox, [[1.0, 1.0, 0.0], [0.0, 1.0, 1.0]]))
+    (outc * _t(ox, [1.0, 2.0, 3.0, 4.0])).sum(0).backward()
+    assert col.grad.numpy().ravel().tolist() == [3.0, 7.0]
+
+
+def test_index_select_gradcheck_and_duplicate_accumulation(ox):
+    a = rng_vec(12, 15).reshape(4, 3)
+    check_with_weights(ox, a, rng_vec(6, 16).reshape(2, 3), lambda x: x.index_select(0, [2, 0]))
+    x = _t(ox, np.zeros((4, 3)), True)
+    g = _t(ox, [[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]])
+    (x.index_select(0, [1, 1]) * g).sum(0).sum(0).backward()
+    assert x.grad.numpy().tolist() == [[0, 0, 0], [5, 7, 9], [0, 0, 0], [0, 0, 0]]
+
+
+def test_rng_vec_matches_the_reference_generator():
+    """The first draws of tests.rs:83-95 for seed 1, worked by hand from the
+    xorshift64 steps (13, 7, 17) and the (state % 2000) / 1000 - 1 mapping."""
+    mask = (1 << 64) - 1
+    s = 1
+    s ^= (s << 13) & mask
+    s ^= s >> 7
+    s ^= (s << 17) & mask
+    assert s == 1082269761
+    assert rng_vec(1, 1)[0] == np.float32(1082269761 % 2000) / np.float32(1000) - np.float32(1)
+    # the state starts at seed | 1, so seeds 2 and 3 draw the same values
+    assert np.array_equal(rng_vec(6, 2), rng_vec(6, 3))
