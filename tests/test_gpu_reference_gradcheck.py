@@ -174,3 +174,77 @@ def test_rng_vec_matches_the_reference_generator():
     assert rng_vec(1, 1)[0] == np.float32(1082269761 % 2000) / np.float32(1000) - np.float32(1)
     # the state starts at seed | 1, so seeds 2 and 3 draw the same values
     assert np.array_equal(rng_vec(6, 2), rng_vec(6, 3))
+
+
+# ---- the rest of crates/oxi-autograd/src/tests.rs ----------------------------------------------
+
+def test_second_order_gradient(ox):
+    """tests.rs:378-426: central differences of the first-order gradient of
+    sum(sigmoid(x)^2) match f'' = 2 s^2 (1 - s)(2 - 3 s) within 1e-2."""
+    a = np.array([[0.3, -0.4], [0.9, -1.1]], np.float32)
+
+    def grad_at(v):
+        x = _t(ox, v, True)
+        s = x.apply("sigmoid")
+        (s * s).sum(0).sum(0).backward()
+        return x.grad.numpy().ravel()
+
+    for i in range(4):
+        plus, minus = a.ravel().copy(), a.ravel().copy()
+        plus[i] += H
+        minus[i] -= H
+        second_numeric = (grad_at(plus.reshape(2, 2))[i] - grad_at(minus.reshape(2, 2))[i]) / (2.0 * H)
+        s = 1.0 / (1.0 + np.exp(-a.ravel()[i]))
+        analytic_second = 2.0 * s * s * (1.0 - s) * (2.0 - 3.0 * s)
+        assert abs(second_numeric - analytic_second) < 1e-2, (i, second_numeric, analytic_second)
+
+
+def test_implicit_seed_accepts_one_element(ox):
+    """graph.rs:381: a root of one element (shape [1] here) seeds with ones."""
+    w = _t(ox, [2.0], True)
+    (w * w).sum(0).backward()  # a 0-d root
+    v = _t(ox, [[3.0]], True)
+    (v * v).sum(0).backward()  # shape [1]
+    assert v.grad.numpy().tolist() == [[6.0]] and w.grad.numpy().tolist() == [4.0]
+
+
+def test_sgd_trains_linear_regression(ox):
+    """tests.rs:619-660 through the device SGD: x @ w for (8, 1) x (1, 1) is
+    the broadcast product; the loss is the reference's shape-[1] column sum."""
+    from oxitorch_amd import optim
+    from oxitorch_amd.nn import Parameter
+
+    xs = (np.arange(8, dtype=np.float32) * 0.5 - 1.5).reshape(8, 1)
+    x, y = _t(ox, xs), _t(ox, 2.0 * xs + 1.0)
+    w, b = Parameter(_t(ox, [[0.5]], True)), Parameter(_t(ox, [0.0], True))
+    opt = optim.Sgd([w, b], lr=0.05)
+
+    def loss_of():
+        diff = x * w.tensor + b.tensor - y
+        return (diff * diff).sum(0)
+
+    first = None
+    for _ in range(200):
+        loss = loss_of()
+        if first is None:
+            first = float(loss.numpy()[0])
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+    final = float(loss_of().numpy()[0])
+    assert final < first * 1e-4, (first, final)
+    assert abs(float(w.tensor.numpy().ravel()[0]) - 2.0) < 0.05
+    assert abs(float(b.tensor.numpy()[0]) - 1.0) < 0.05
+
+
+def test_no_grad_results_bridge_back_into_graded_code(ox):
+    """tests.rs:538-552 with w @ w replaced by w * w: a result computed under
+    no_grad is a constant in later graded code and gets no gradient."""
+    w = _t(ox, [[1.0, 2.0], [3.0, 4.0]], True)
+    with ox.no_grad():
+        frozen = w * w
+    assert not frozen.requires_grad
+    x = _t(ox, np.full((2, 2), 0.5), True)
+    (x * frozen).sum(0).sum(0).backward()
+    assert x.grad is not None
+    assert w.grad is None, "frozen subgraph gets no gradient"
