@@ -10,8 +10,11 @@
 //   rows    the innermost dim is contiguous or broadcast for every operand:
 //           one block walks a chunk of one row, offsets computed once per row;
 //   tiled   an input is transposed relative to the output (its unit-stride
-//           dim is not the output's innermost dim): 64x64 tiles staged
-//           through LDS so both the transposed read and the write coalesce;
+//           dim is not the output's innermost dim). With float4-aligned
+//           operands one wave owns a 32x32 tile and each lane a 4x4 block,
+//           read as float4 rows along the input's unit-stride dim and
+//           written as float4 columns along the output's innermost dim, so
+//           both coalesce with no LDS; otherwise 64x64 tiles go through LDS;
 //   generic anything else: per-element index arithmetic.
 #include <algorithm>
 #include <cstring>
@@ -207,24 +210,20 @@ __global__ __launch_bounds__(BS) void map_tiled_k(F f, Plan<N> p, int jd, unsign
   }
 }
 
-// tiled, float4 flavour: same 64x64 tiles, every global access a 16-byte
-// vector (4 consecutive elements along the transposed input's unit-stride
-// dim when loading, along the output's innermost dim when storing). TM (the
-// transposed-input mask) is a template parameter so that LDS holds tiles for
-// the transposed inputs only; block indices are decoded in 32-bit arithmetic.
-template <int N, unsigned TM>
-constexpr int tile_slot(int k) {
-  int s = 0;
-  for (int q = 0; q < k; ++q) s += (TM >> q) & 1u;
-  return s;
-}
+// tiled in registers: one wave per 32 x 32 tile, lanes on an 8 x 8 grid, each
+// lane a 4 (jd) x 4 (innermost) block. A transposed input is read as 4
+// float4 rows along its unit-stride dim; the output is written as 4 float4
+// columns along its innermost dim; the transpose between them is only which
+// register goes where. Each load or store instruction of a wave covers 8
+// runs of 128 contiguous bytes; no LDS, no barriers.
+constexpr int RT = 32;  // tile extent per wave in both dims
 
 template <class F, int N, unsigned TM, bool NTS>
-__global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, unsigned tiles_d, unsigned tiles_j) {
-  constexpr int NTR = tile_slot<N, TM>(N);  // number of transposed inputs
-  __shared__ float tile[NTR][T][T + 1];
+__global__ __launch_bounds__(BS) void map_regt_k(F f, Plan<N> p, int jd, unsigned tiles_d, unsigned tiles_j,
+                                                 unsigned tiles) {
+  unsigned b = blockIdx.x * (BS / 64) + (threadIdx.x >> 6);  // this wave's tile
+  if (b >= tiles) return;
   const int d = p.ndim - 1;
-  unsigned b = blockIdx.x;
   const unsigned td = b % tiles_d;
   b /= tiles_d;
   const unsigned tj = b % tiles_j;
@@ -240,68 +239,54 @@ __global__ __launch_bounds__(BS) void map_tiled_vec_k(F f, Plan<N> p, int jd, un
 #pragma unroll
     for (int k = 0; k <= N; ++k) off[k] += (int64_t)c * p.st[k][q];
   }
-  const int j0 = (int)tj * T, d0 = (int)td * T;
-  const int nj = (int)p.shape[jd], nd = (int)p.shape[d];
-  const int t = threadIdx.x;
-  // loads of transposed inputs: 16 lanes cover 64 consecutive j of one d
+  const int lane = threadIdx.x & 63;
+  const int gj = (int)tj * RT + 4 * (lane & 7), gd = (int)td * RT + 4 * (lane >> 3);
+  // both dims are multiples of 4: a block is wholly inside or wholly outside
+  if (gj >= (int)p.shape[jd] || gd >= (int)p.shape[d]) return;
+  float v[N][4][4];  // [input][jd offset c][innermost offset r]
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    if constexpr (true) {
-      if (!((TM >> k) & 1u)) continue;
-    }
     const float* q = p.x[k] + off[k + 1];
-    const int64_t sd = p.st[k + 1][d];
+    if ((TM >> k) & 1u) {
+      const int64_t sd = p.st[k + 1][d];
 #pragma unroll
-    for (int i = 0; i < (T * T / 4) / BS; ++i) {
-      const int l = i * BS + t;
-      const int jj = (l % (T / 4)) * 4, dd = l / (T / 4);
-      const int gj = j0 + jj, gd = d0 + dd;
-      f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (gj < nj && gd < nd) v = ld_stream(reinterpret_cast<const f4*>(q + gj + gd * sd));
-      float* row = &tile[tile_slot<N, TM>(k)][dd][jj];
-      row[0] = v.x;
-      row[1] = v.y;
-      row[2] = v.z;
-      row[3] = v.w;
-    }
-  }
-  __syncthreads();
-  // compute + store: 16 lanes cover 64 consecutive d of one j
+      for (int r = 0; r < 4; ++r) {
+        const f4 t = ld_stream(reinterpret_cast<const f4*>(q + gj + (int64_t)(gd + r) * sd));
 #pragma unroll
-  for (int i = 0; i < (T * T / 4) / BS; ++i) {
-    const int l = i * BS + t;
-    const int dd = (l % (T / 4)) * 4, jj = l / (T / 4);
-    const int gj = j0 + jj, gd = d0 + dd;
-    if (gj >= nj || gd >= nd) continue;
-    f4 in[N];
+        for (int c = 0; c < 4; ++c) v[k][c][r] = t[c];
+      }
+    } else {
+      const int64_t sj = p.st[k + 1][jd];
+      const bool bc = p.st[k + 1][d] == 0;
 #pragma unroll
-    for (int k = 0; k < N; ++k) {
-      if ((TM >> k) & 1u) {
-        const int ts = tile_slot<N, TM>(k);
-        in[k] = f4{tile[ts][dd][jj], tile[ts][dd + 1][jj], tile[ts][dd + 2][jj], tile[ts][dd + 3][jj]};
-      } else {
-        const float* q = p.x[k] + off[k + 1] + (int64_t)gj * p.st[k + 1][jd];
-        if (p.st[k + 1][d] == 0) in[k] = f4{q[0], q[0], q[0], q[0]};
-        else in[k] = *reinterpret_cast<const f4*>(q + gd);
+      for (int c = 0; c < 4; ++c) {
+        const float* row = q + (int64_t)(gj + c) * sj;
+        const f4 t = bc ? f4{row[0], row[0], row[0], row[0]} : *reinterpret_cast<const f4*>(row + gd);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[k][c][r] = t[r];
       }
     }
-    f4 r;
+  }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float v[N];
+  for (int c = 0; c < 4; ++c) {
+    f4 o;
 #pragma unroll
-      for (int k = 0; k < N; ++k) v[k] = in[k][c];
-      r[c] = apply<F, N>(f, v);
+    for (int r = 0; r < 4; ++r) {
+      float a[N];
+#pragma unroll
+      for (int k = 0; k < N; ++k) a[k] = v[k][c][r];
+      o[r] = apply<F, N>(f, a);
     }
-    st_stream<NTS>(r, reinterpret_cast<f4*>(p.y + off[0] + (int64_t)gj * p.st[0][jd] + gd));
+    st_stream<NTS>(o, reinterpret_cast<f4*>(p.y + off[0] + (int64_t)(gj + c) * p.st[0][jd] + gd));
   }
 }
 
 template <class F, int N, unsigned TM>
-void launch_tiled_vec(F f, const Plan<N>& p, int jd, unsigned blocks, unsigned tiles_d, unsigned tiles_j, bool nts,
-                      hipStream_t s) {
-  if (nts) map_tiled_vec_k<F, N, TM, true><<<dim3(blocks), dim3(BS), 0, s>>>(f, p, jd, tiles_d, tiles_j);
-  else map_tiled_vec_k<F, N, TM, false><<<dim3(blocks), dim3(BS), 0, s>>>(f, p, jd, tiles_d, tiles_j);
+void launch_regt(F f, const Plan<N>& p, int jd, unsigned tiles_d, unsigned tiles_j, unsigned tiles, bool nts,
+                 hipStream_t s) {
+  const unsigned blocks = (tiles + BS / 64 - 1) / (BS / 64);
+  if (nts) map_regt_k<F, N, TM, true><<<dim3(blocks), dim3(BS), 0, s>>>(f, p, jd, tiles_d, tiles_j, tiles);
+  else map_regt_k<F, N, TM, false><<<dim3(blocks), dim3(BS), 0, s>>>(f, p, jd, tiles_d, tiles_j, tiles);
 }
 
 // ---------------------------------------------------------------------------
@@ -507,12 +492,14 @@ int launch_map(F f, const char* what, float* y, const int64_t* ys, const float* 
         // 32-bit block decode: every dim and the block count stay below 2^31
         for (int q = 0; q < p.ndim && vec; ++q)
           if (p.shape[q] >= ((int64_t)1 << 31)) vec = false;
-        if (vec) {
-          const unsigned nb = (unsigned)blocks, ntd = (unsigned)tiles_d, ntj = (unsigned)tiles_j;
-          if (tmask == 1u) launch_tiled_vec<F, N, 1u>(f, p, jd, nb, ntd, ntj, nts, s);
+        const int64_t rtiles = ceil_div(p.shape[d], RT) * ceil_div(p.shape[jd], RT) * batch;
+        if (vec && rtiles < ((int64_t)1 << 31)) {
+          const unsigned ntd = (unsigned)ceil_div(p.shape[d], RT), ntj = (unsigned)ceil_div(p.shape[jd], RT);
+          const unsigned nt = (unsigned)rtiles;
+          if (tmask == 1u) launch_regt<F, N, 1u>(f, p, jd, ntd, ntj, nt, nts, s);
           else if constexpr (N == 2) {
-            if (tmask == 2u) launch_tiled_vec<F, N, 2u>(f, p, jd, nb, ntd, ntj, nts, s);
-            else launch_tiled_vec<F, N, 3u>(f, p, jd, nb, ntd, ntj, nts, s);
+            if (tmask == 2u) launch_regt<F, N, 2u>(f, p, jd, ntd, ntj, nt, nts, s);
+            else launch_regt<F, N, 3u>(f, p, jd, ntd, ntj, nt, nts, s);
           }
         } else
           map_tiled_k<F, N><<<dim3((unsigned)blocks), dim3(BS), 0, s>>>(f, p, jd, tmask, tiles_d, tiles_j);
