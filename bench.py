@@ -44,10 +44,17 @@ METRIC = "achieved HBM GB/s (% of MI355X peak) + rows/s, norm/softmax/embed fwd+
 
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled
 # by the same counters' reading of a 1 GiB copy (FETCH x2.0, WRITE x1.0);
-# the runs and the per-kernel tables are in profiles/pmc_traffic_c2.md,
-# profiles/pmc_traffic_f3.md and profiles/pmc_traffic_f4.md.
+# the runs and the per-kernel tables are in profiles/pmc_traffic_<config>.md.
+MIB = 1 << 20
 TRAFFIC_BYTES = {
+    # profiles/pmc_traffic_c1.md: norm_bwd_k + col_finish_k
+    "c1": {"rms_norm_bwd": (36.9 + 0.8) * MIB},
     "c2": {"layer_norm_fwd": 538.2e6, "gelu_erf_fwd": 537.0e6, "gelu_erf_bwd": 805.5e6, "layer_norm_bwd": 840.2e6},
+    # profiles/pmc_traffic_c3.md
+    "c3": {"cross_entropy_bwd": 2001.6 * MIB},
+    # profiles/pmc_traffic_c4.md and pmc_traffic_c5.md: seg_wave_k + seg_fixup_k
+    "c4": {"embedding_bwd": (718.5 + 6.6) * MIB},
+    "c5": {"embedding_bwd": (197.4 + 0.0) * MIB},
     # profiles/pmc_traffic_f3.md: all launches of each C-ABI call
     "f3": {"masked_select_fwd": 970.8e6, "masked_select_bwd": 425.7e6, "scatter_rows_fwd": 311.2e6,
            "scatter_rows_bwd": 407.3e6},
