@@ -57,7 +57,7 @@ TRAFFIC_BYTES = {
     "c5": {"embedding_bwd": (197.4 + 0.0) * MIB},
     # profiles/pmc_traffic_f3.md: all launches of each C-ABI call
     "f3": {"masked_select_fwd": 970.8e6, "masked_select_bwd": 425.7e6, "scatter_rows_fwd": 311.2e6,
-           "scatter_rows_bwd": 407.3e6},
+           "scatter_rows_bwd": 363.9e6},
     # profiles/pmc_traffic_f4.md: the 5 launches of one multi-parameter call
     "f4": {"adamw_step_multi": 3484.9e6},
 }

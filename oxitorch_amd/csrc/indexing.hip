@@ -81,7 +81,10 @@ __global__ __launch_bounds__(BS) void scatter_rows_k(const float* __restrict__ b
 
 // VJP in one launch: units [0, gb_units) give gbase = g * (written ? 0 : 1);
 // the rest give gvalues slot p = g row idx[p] when p won that row, else 0.
-template <bool VEC, bool NARROW>
+// FUSED (both outputs wanted): a base unit whose row was written also stores
+// its g value into the winning slot of gvalues, so each row of g is read
+// once, and the gvalues units only write the zeros of the slots that lost.
+template <bool VEC, bool NARROW, bool FUSED>
 __global__ __launch_bounds__(BS) void scatter_rows_bwd_k(const float* __restrict__ g, const int64_t* __restrict__ idx,
                                                          const int* __restrict__ w, float* __restrict__ gbase,
                                                          float* __restrict__ gvalues, int64_t rows, int64_t iu,
@@ -91,16 +94,20 @@ __global__ __launch_bounds__(BS) void scatter_rows_bwd_k(const float* __restrict
   if (u < gb_units) {
     int64_t r, c0;
     row_col<NARROW>(u, iu, &r, &c0);
-    const float m = w[r] ? 0.0f : 1.0f;
+    const int win = w[r];  // winning position + 1, 0 when the row keeps its base value
+    const float m = win ? 0.0f : 1.0f;
     if constexpr (VEC) {
       f4 v = ld_stream(reinterpret_cast<const f4*>(g) + u);
+      if (FUSED && win) reinterpret_cast<f4*>(gvalues)[(int64_t)(win - 1) * iu + c0] = v;
       v.x = v.x * m;
       v.y = v.y * m;
       v.z = v.z * m;
       v.w = v.w * m;
       reinterpret_cast<f4*>(gbase)[u] = v;
     } else {
-      gbase[u] = g[u] * m;
+      const float v = g[u];
+      if (FUSED && win) gvalues[(int64_t)(win - 1) * iu + c0] = v;
+      gbase[u] = v * m;
     }
     return;
   }
@@ -110,6 +117,7 @@ __global__ __launch_bounds__(BS) void scatter_rows_bwd_k(const float* __restrict
   int64_t r = idx[p];
   if (r < 0) r += rows;
   const bool won = r >= 0 && r < rows && w[r] == (int)(p + 1);
+  if (FUSED && won) return;  // stored by the base unit of row r
   if constexpr (VEC) {
     reinterpret_cast<f4*>(gvalues)[q] = won ? reinterpret_cast<const f4*>(g)[r * iu + c] : f4{0.f, 0.f, 0.f, 0.f};
   } else {
@@ -623,12 +631,20 @@ int oxi_scatter_rows_bwd(const float* g, int64_t rows, int64_t inner, const int6
   hipStream_t s = stream();
   const unsigned blocks = (unsigned)ceil_div(units, BS);
   const bool narrow = blocks * (int64_t)BS <= (int64_t)UINT32_MAX;
-  if (vec && narrow)
-    scatter_rows_bwd_k<true, true><<<blocks, BS, 0, s>>>(g, idx, w, gbase, gvalues, rows, iu, gb_units, units);
-  else if (vec)
-    scatter_rows_bwd_k<true, false><<<blocks, BS, 0, s>>>(g, idx, w, gbase, gvalues, rows, iu, gb_units, units);
-  else
-    scatter_rows_bwd_k<false, false><<<blocks, BS, 0, s>>>(g, idx, w, gbase, gvalues, rows, iu, gb_units, units);
+  const bool fused = gbase && gvalues;
+#define OXI_SRB(V, NW, FU) \
+  scatter_rows_bwd_k<V, NW, FU><<<blocks, BS, 0, s>>>(g, idx, w, gbase, gvalues, rows, iu, gb_units, units)
+  if (vec && narrow) {
+    if (fused) OXI_SRB(true, true, true);
+    else OXI_SRB(true, true, false);
+  } else if (vec) {
+    if (fused) OXI_SRB(true, false, true);
+    else OXI_SRB(true, false, false);
+  } else {
+    if (fused) OXI_SRB(false, false, true);
+    else OXI_SRB(false, false, false);
+  }
+#undef OXI_SRB
   return check_launch("scatter_rows_bwd");
 }
 
