@@ -3,8 +3,9 @@
 // crates/oxi-tensor/src/lib.rs:665-703; scatter_index_select:
 // crates/oxi-autograd/src/ops.rs:741-769).
 //
-// Gather: out[o, k, :] = src[o, idx[k], :]. Each block copies 8 rows per step
-// with float4 accesses (8 independent loads in flight per thread).
+// Gather: out[o, k, :] = src[o, idx[k], :]. Each block copies GRPB (2) rows
+// with float4 accesses, the rows' loads issued together; threads per block
+// are the row's float4 count rounded up to whole waves.
 //
 // VJP without float atomics (6 launches for 16-bit keys):
 //   1. stable LSD radix sort of (key, position) by 8-bit digits, a histogram
@@ -661,6 +662,12 @@ int check_sizes(const char* what, int64_t outer, int64_t len, int64_t inner, int
   if (outer < 0 || len < 0 || inner < 0 || n < 0) return fail(OXI_INVALID_ARGUMENT, "%s: negative size", what);
   if (len >= ((int64_t)1 << 31) - 1 || n >= ((int64_t)1 << 31) - 1)
     return fail(OXI_INVALID_ARGUMENT, "%s: index space exceeds the kernel limits", what);
+  // element counts (outer * max(len, n) * inner) must stay well inside int64
+  const int64_t rows = std::max(len, n);
+  const int64_t limit = (int64_t)1 << 60;
+  if (outer && rows && inner && (outer > limit / rows || outer * rows > limit / inner))
+    return fail(OXI_INVALID_ARGUMENT, "%s: size (%lld, %lld, %lld) exceeds the kernel limits", what,
+                (long long)outer, (long long)rows, (long long)inner);
   return OXI_OK;
 }
 

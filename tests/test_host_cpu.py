@@ -61,6 +61,11 @@ def test_argument_errors_map_to_value_error():
         capi.call("oxi_rms_norm_fwd", None, None, None, None, -1, 4, 1e-6)
     with pytest.raises(ValueError, match="unknown VJP mode"):
         capi.call("oxi_layer_norm_bwd", None, None, None, None, None, None, None, None, 0, 4, 7)
+    # element counts that would overflow the kernels' 64-bit index arithmetic
+    with pytest.raises(ValueError, match="exceeds the kernel limits"):
+        capi.call("oxi_index_select", None, 1 << 40, 1 << 20, 1 << 20, None, 4, None)
+    with pytest.raises(ValueError, match="exceeds the kernel limits"):
+        capi.call("oxi_index_select_bwd", None, 1, 1 << 30, 1 << 32, None, 4, None)
 
 
 def test_oracle_is_not_imported_by_the_product():
