@@ -323,6 +323,7 @@ int build_plan(Plan<N>& p, float* y, const int64_t* ys, const float* const* xs, 
   int64_t n = 1;
   for (int d = 0; d < ndim; ++d) {
     if (shape[d] < 0) return fail(OXI_INVALID_ARGUMENT, "negative dim size %lld", (long long)shape[d]);
+    if (shape[d] && n > (((int64_t)1 << 60) / shape[d])) return fail(OXI_INVALID_ARGUMENT, "element count exceeds the kernel limits");
     n *= shape[d];
   }
   *numel = n;

@@ -220,8 +220,12 @@ int oxi_reduce(int kind, const float* x, const int64_t* xs, const int64_t* shape
   RPlan p;
   p.nd = 0;
   int64_t nout = 1;
+  int64_t total = 1;
   for (int d = 0; d < ndim; ++d) {
     if (shape[d] < 0) return fail(OXI_INVALID_ARGUMENT, "reduce: negative dim size");
+    if (shape[d] && total > (((int64_t)1 << 60) / shape[d]))
+      return fail(OXI_INVALID_ARGUMENT, "reduce: element count exceeds the kernel limits");
+    total *= shape[d];
     if (d == dim) continue;
     p.size[p.nd] = shape[d];
     p.st[p.nd] = xs[d];

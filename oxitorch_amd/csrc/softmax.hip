@@ -337,7 +337,10 @@ bool aligned16(std::initializer_list<const void*> ps) {
 int check_olen(const char* what, int64_t outer, int64_t len, int64_t inner, std::initializer_list<const void*> ps) {
   if (outer < 0 || len < 0 || inner < 0)
     return fail(OXI_INVALID_ARGUMENT, "%s: negative size", what);
-  if (len > ((int64_t)1 << 30) || outer * inner > ((int64_t)1 << 40))
+  // len and outer * inner each bounded, and the element count inside int64
+  const int64_t lim = (int64_t)1 << 40;
+  if (len > ((int64_t)1 << 30) || (outer && inner > lim / outer) ||
+      (outer && inner && len > (((int64_t)1 << 60) / outer) / inner))
     return fail(OXI_INVALID_ARGUMENT, "%s: size exceeds the kernel limits", what);
   if (outer && len && inner)
     for (const void* p : ps)

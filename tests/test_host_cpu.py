@@ -66,6 +66,14 @@ def test_argument_errors_map_to_value_error():
         capi.call("oxi_index_select", None, 1 << 40, 1 << 20, 1 << 20, None, 4, None)
     with pytest.raises(ValueError, match="exceeds the kernel limits"):
         capi.call("oxi_index_select_bwd", None, 1, 1 << 30, 1 << 32, None, 4, None)
+    with pytest.raises(ValueError, match="exceeds the kernel limits"):
+        capi.call("oxi_softmax_fwd", None, None, 1 << 31, 1 << 30, 1)  # 2^61 elements
+    big = capi._i64arr([1 << 31, 1 << 31])  # 2^62 elements
+    st = capi._i64arr([0, 0])
+    with pytest.raises(ValueError, match="exceeds the kernel limits"):
+        capi.call("oxi_unary", 0, None, st, None, st, big, 2)
+    with pytest.raises(ValueError, match="exceeds the kernel limits"):
+        capi.call("oxi_reduce", 0, None, st, big, 2, 1, None)
 
 
 def test_oracle_is_not_imported_by_the_product():
