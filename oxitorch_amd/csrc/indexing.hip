@@ -564,6 +564,7 @@ int grid_size(const int64_t* shape, int ndim, int64_t* E, int64_t* T, const char
   int64_t e = 1;
   for (int d = 0; d < ndim; ++d) {
     if (shape[d] < 0) return fail(OXI_INVALID_ARGUMENT, "%s: negative dim size", what);
+    if (shape[d] && e > (((int64_t)1 << 60) / shape[d])) return fail(OXI_INVALID_ARGUMENT, "%s: grid too large", what);
     e *= shape[d];
   }
   *E = e;
@@ -585,6 +586,8 @@ int oxi_scatter_rows(const float* base, int64_t rows, int64_t inner, const int64
                      const float* values, float* out) {
   if (rows < 0 || inner < 0 || n < 0) return fail(OXI_INVALID_ARGUMENT, "scatter_rows: negative size");
   if (n >= INT32_MAX) return fail(OXI_INVALID_ARGUMENT, "scatter_rows: too many positions (%lld)", (long long)n);
+  if (inner && (rows + n) > (((int64_t)1 << 60) / inner))
+    return fail(OXI_INVALID_ARGUMENT, "scatter_rows: size exceeds the kernel limits");
   if (rows == 0 && n > 0) return fail(OXI_INVALID_ARGUMENT, "scatter_rows: positions into an empty tensor");
   if (rows == 0 || inner == 0) return OXI_OK;
   if (!base || !out || (n > 0 && (!idx || !values)))
@@ -613,6 +616,8 @@ int oxi_scatter_rows_bwd(const float* g, int64_t rows, int64_t inner, const int6
                          float* gvalues) {
   if (rows < 0 || inner < 0 || n < 0) return fail(OXI_INVALID_ARGUMENT, "scatter_rows_bwd: negative size");
   if (n >= INT32_MAX) return fail(OXI_INVALID_ARGUMENT, "scatter_rows_bwd: too many positions (%lld)", (long long)n);
+  if (inner && (rows + n) > (((int64_t)1 << 60) / inner))
+    return fail(OXI_INVALID_ARGUMENT, "scatter_rows_bwd: size exceeds the kernel limits");
   if (inner == 0 || (rows == 0 && n == 0)) return OXI_OK;
   if (rows == 0) return fail(OXI_INVALID_ARGUMENT, "scatter_rows_bwd: positions into an empty tensor");
   if (!g || (n > 0 && !idx)) return fail(OXI_INVALID_ARGUMENT, "scatter_rows_bwd: NULL pointer");

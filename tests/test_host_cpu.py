@@ -52,6 +52,8 @@ def test_no_device_is_an_error_not_a_fallback():
 
 
 def test_argument_errors_map_to_value_error():
+    import ctypes
+
     from oxitorch_amd import capi
 
     # validated before any device use
@@ -74,6 +76,10 @@ def test_argument_errors_map_to_value_error():
         capi.call("oxi_unary", 0, None, st, None, st, big, 2)
     with pytest.raises(ValueError, match="exceeds the kernel limits"):
         capi.call("oxi_reduce", 0, None, st, big, 2, 1, None)
+    with pytest.raises(ValueError, match="exceeds the kernel limits"):
+        capi.call("oxi_scatter_rows", None, 1 << 40, 1 << 30, None, 0, None, None)
+    with pytest.raises(ValueError, match="grid too large"):
+        capi.call("oxi_masked_select_record_bytes", big, 2, ctypes.byref(ctypes.c_int64()))
 
 
 def test_oracle_is_not_imported_by_the_product():
