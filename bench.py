@@ -7,7 +7,9 @@ liboxihip C-ABI (include/oxihip.h) in the order the host core launches it.
 Default workload: config 2, F.layer_norm(affine) -> exact-erf gelu, fwd+bwd,
 fp32, x (16384, 4096). `--config c1|c3|c4|c5` selects the other configs;
 `--config f2` times device DataLoader batches (the step before the path),
-`--config f3` masked_select and the row scatter (fwd+bwd), and
+`--config f3` masked_select and the row scatter (fwd+bwd), `--config c2f` the
+C2 step with the fused layer_norm+gelu VJP the graph uses by default (the
+default C2 line also reports it under "fused_vjp"), and
 `--config f4` one AdamW step over GPT-2 small's 148 parameter tensors (the
 optimizer step after backward).
 
@@ -182,6 +184,23 @@ class C2(Workload):
                                                               self.dh.ptr, self.dx.ptr, self.dw.ptr, self.db.ptr, R,
                                                               H, 0)), 3 * E4)]
 
+    # The graph's default for this config: when the norm output feeds only the
+    # GELU, backward runs both VJPs as one pass (oxi_layer_norm_act_bwd reads
+    # x and g, writes dy and dx), so a step crosses HBM 8 E-sized times, not
+    # 10. The step above is the path with that fusion off (OXI_FUSE_NORM_ACT=0)
+    # or with other consumers of the norm output; it is the per-op byte count
+    # the metric is defined on.
+    fused_what = ("layer_norm_fwd + gelu_erf_fwd + oxi_layer_norm_act_bwd (the graph's default backward for "
+                  "gelu(layer_norm(x)))")
+
+    def fused_kernels(self):
+        L, c, R, H = self.hip.lib, self.hip.check, self.R, self.H
+        E4 = R * H * 4
+        return C2.kernels(self)[:2] + [
+            ("layer_norm_gelu_bwd", lambda: c(L.oxi_layer_norm_act_bwd(
+                self.x.ptr, self.w.ptr, self.b.ptr, self.mean.ptr, self.rstd.ptr, self.g.ptr, 1, self.dh.ptr,
+                self.dx.ptr, self.dw.ptr, self.db.ptr, R, H, 0)), 4 * E4)]
+
     def cpu_step(self, ref, lo, hi):
         h = self.host
         x, g = h["x"][lo:hi], h["g"][lo:hi]
@@ -189,6 +208,19 @@ class C2(Workload):
         ref.gelu_erf_fwd(hh)
         dh = ref.gelu_erf_bwd(hh, g)
         ref.layer_norm_bwd(x, h["w"], mu, inv, dh)
+
+
+class C2F(C2):
+    """C2 as the graph runs it by default (the norm output feeds only the
+    GELU): the forward kernels of C2, then one pass for both VJPs."""
+
+    def __init__(self, hip):
+        super().__init__(hip)
+        self.name = "C2 layer_norm(affine)+erf-gelu fwd+bwd fp32 x(16384,4096), fused layer_norm+gelu VJP"
+        self.bytes_per_step = 8 * self.R * self.H * 4
+
+    def kernels(self):
+        return self.fused_kernels()
 
 
 class C3(Workload):
@@ -565,7 +597,7 @@ class F3(Workload):
         ref.scatter_dim0_bwd(h["gs"], h["ids"], h["vals"].shape)
 
 
-WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f2": F2, "f3": F3, "f4": F4}
+WORKLOADS = {"c1": C1, "c2": C2, "c2f": C2F, "c3": C3, "c4": C4, "c5": C5, "f2": F2, "f3": F3, "f4": F4}
 
 
 # ---------------------------------------------------------------------------
@@ -771,6 +803,23 @@ def main():
                      "algorithmic_bytes": d["bytes"]},
         "cpu_baseline": None,
     }
+    if hasattr(wl, "fused_kernels") and not isinstance(wl, C2F):
+        fk = wl.fused_kernels()
+        for _ in range(max(args.warmup, 1)):
+            for _, fn, _ in fk:
+                fn()
+        hip.sync()
+        log("timing the fused-VJP variant")
+        fms = time_steps(hip, fk, args.steps, [])
+        fper = time_kernels(hip, fk, max(3, min(args.steps, 10)))
+        fbytes = sum(b for _, _, b in fk)
+        line["fused_vjp"] = {
+            "what": wl.fused_what, "ms_per_step": round(fms, 5), "algorithmic_bytes_per_step": fbytes,
+            "gbs": round(fbytes / (fms * 1e-3) / 1e9, 2),
+            "pct_of_peak": round(100.0 * fbytes / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+            "rows_per_s": round(wl.rows / (fms * 1e-3), 1),
+            "kernels": {k: {"avg_ms": round(v["ms"], 5), "gbs": None if v["gbs"] is None else round(v["gbs"], 1)}
+                        for k, v in fper.items()}}
     log("cold-cache median")
     ms_cold = time_cold(hip, kernels)
     line["cold_cache"] = {"ms_per_step_median_of_20": round(ms_cold, 5),

@@ -78,6 +78,10 @@ enum { OXI_NORM_VJP_REF = 0, OXI_NORM_VJP_EXACT = 1 };
  * the exact 0.5x(1+erf(x/sqrt2)) that the reference lacks. */
 enum { OXI_GELU_TANH = 0, OXI_GELU_ERF = 1 };
 
+/* Activations a norm VJP can absorb (oxi_*_norm_act_bwd). The two GELU values
+ * equal OXI_GELU_*. */
+enum { OXI_ACT_GELU_TANH = 0, OXI_ACT_GELU_ERF = 1, OXI_ACT_SILU = 2 };
+
 /* ------------------------------------------------------------------------ */
 /* Runtime: device identity, memory, stream.                                */
 /* Replaces the CPU-only device seam: Tensor::device (crates/oxi-tensor/src/lib.rs:192-196),
@@ -217,6 +221,25 @@ int oxi_layer_norm_fwd(const float* x, const float* w, const float* b, float* y,
 int oxi_layer_norm_bwd(const float* x, const float* w, const float* mean, const float* rstd,
                        const float* g, float* dx, float* dw, float* db,
                        int64_t rows, int64_t cols, int mode);
+/* The VJPs of act(norm(x)) in one pass, for a graph where the norm's output y
+ * feeds only the activation `act` (OXI_ACT_*). They replace the activation's
+ * VJP followed by the norm's, which the reference runs as two graph nodes in
+ * reverse topological order (crates/oxi-autograd/src/graph.rs:398-436: the
+ * activation node's VJP accumulates y's gradient, the norm node's VJP reads
+ * it). `g` is the gradient of act(y). y is recomputed from x and the saved
+ * statistics with the forward's arithmetic; dy = g * act'(y) is the value
+ * oxi_gelu_bwd/oxi_silu_bwd write and is stored to `dy` unless NULL (it is
+ * y's gradient, which the graph keeps); dx/dw/db are what the matching
+ * oxi_*_norm_bwd computes from dy, bit for bit. Each row then crosses HBM four
+ * times (read x and g, write dy and dx) instead of six.
+ * Returns OXI_NOT_IMPLEMENTED and writes nothing when a row does not
+ * vectorize (cols % 4 != 0, cols > 8192, or a pointer not 16-byte aligned):
+ * the caller then runs the two VJPs. */
+int oxi_rms_norm_act_bwd(const float* x, const float* w, const float* rstd, const float* g, int act,
+                         float* dy, float* dx, float* dw, int64_t rows, int64_t cols, int mode);
+int oxi_layer_norm_act_bwd(const float* x, const float* w, const float* b, const float* mean,
+                           const float* rstd, const float* g, int act, float* dy, float* dx,
+                           float* dw, float* db, int64_t rows, int64_t cols, int mode);
 
 /* ------------------------------------------------------------------------ */
 /* Softmax family over the middle dim of a contiguous (outer, len, inner)    */

@@ -47,6 +47,7 @@ BINARY = ["add", "sub", "mul", "div", "pow", "min", "max", "eq", "ne", "lt", "le
 REDUCE = ["sum", "mean", "max", "min", "argmax", "argmin", "norm"]
 NORM_VJP = {"ref": 0, "exact": 1}
 GELU = {"tanh": 0, "none": 1, "erf": 1}
+ACT = {"gelu_tanh": 0, "gelu_erf": 1, "silu": 2}
 
 _SIGS = {
     "oxi_hip_init": [c_int],
@@ -83,6 +84,8 @@ _SIGS = {
     "oxi_rms_norm_bwd": [vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_layer_norm_fwd": [vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_float],
     "oxi_layer_norm_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
+    "oxi_rms_norm_act_bwd": [vp, vp, vp, vp, c_int, vp, vp, vp, c_i64, c_i64, c_int],
+    "oxi_layer_norm_act_bwd": [vp, vp, vp, vp, vp, vp, c_int, vp, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_softmax_fwd": [vp, vp, c_i64, c_i64, c_i64],
     "oxi_softmax_bwd": [vp, vp, vp, c_i64, c_i64, c_i64],
     "oxi_log_softmax_fwd": [vp, vp, c_i64, c_i64, c_i64],
@@ -337,6 +340,31 @@ def layer_norm_bwd(x, w, mean, rstd, g, mode="ref", need_dx=True, need_dw=True, 
     call("oxi_layer_norm_bwd", x.ptr, w.ptr if w else None, mean.ptr, rstd.ptr, g.ptr, dx.ptr if dx else None,
          dw.ptr if dw else None, db.ptr if db else None, rows, H, NORM_VJP[mode])
     return dx, dw, db
+
+
+def rms_norm_act_bwd(x, w, rstd, g, act, mode="ref", need_dy=True, need_dx=True, need_dw=True):
+    """VJP of act(rms_norm(x)) in one pass; returns (dy, dx, dw). `act` is a key of ACT."""
+    rows, H = _rows(x)
+    dy = DeviceArray(x.shape) if need_dy else None
+    dx = DeviceArray(x.shape) if need_dx else None
+    dw = DeviceArray((H,)) if need_dw else None
+    call("oxi_rms_norm_act_bwd", x.ptr, w.ptr if w else None, rstd.ptr, g.ptr, ACT[act], dy.ptr if dy else None,
+         dx.ptr if dx else None, dw.ptr if dw else None, rows, H, NORM_VJP[mode])
+    return dy, dx, dw
+
+
+def layer_norm_act_bwd(x, w, b, mean, rstd, g, act, mode="ref", need_dy=True, need_dx=True, need_dw=True,
+                       need_db=True):
+    """VJP of act(layer_norm(x)) in one pass; returns (dy, dx, dw, db). `act` is a key of ACT."""
+    rows, H = _rows(x)
+    dy = DeviceArray(x.shape) if need_dy else None
+    dx = DeviceArray(x.shape) if need_dx else None
+    dw = DeviceArray((H,)) if need_dw else None
+    db = DeviceArray((H,)) if need_db else None
+    call("oxi_layer_norm_act_bwd", x.ptr, w.ptr if w else None, b.ptr if b else None, mean.ptr, rstd.ptr, g.ptr,
+         ACT[act], dy.ptr if dy else None, dx.ptr if dx else None, dw.ptr if dw else None, db.ptr if db else None,
+         rows, H, NORM_VJP[mode])
+    return dy, dx, dw, db
 
 
 def _oli(shape, dim):

@@ -384,7 +384,16 @@ Var rms_norm(const Var& x, const Var& w, float eps, NormVjp mode) {
   Tensor y = Tensor::empty(xc.shape, Dev::Hip);
   Tensor rstd = Tensor::empty({rows}, Dev::Hip);
   hip_check(oxi_rms_norm_fwd(xc.data(), wc.data(), y.data(), rstd.data(), rows, H, eps));
-  return Var::op(y, "rms_norm", {x, w}, [xc, wc, rstd, rows, H, mode](const Tensor& g, const std::vector<bool>& need) {
+  auto saved = std::make_shared<NormSaved>();
+  saved->x = xc;
+  saved->w = wc;
+  saved->has_w = true;
+  saved->rstd = rstd;
+  saved->rows = rows;
+  saved->H = H;
+  saved->mode = (int)mode;
+  saved->wi = 1;
+  Var v = Var::op(y, "rms_norm", {x, w}, [xc, wc, rstd, rows, H, mode](const Tensor& g, const std::vector<bool>& need) {
     Grads r(2);
     Tensor gc = t_contiguous(g);
     Tensor dx, dw;
@@ -397,6 +406,8 @@ Var rms_norm(const Var& x, const Var& w, float eps, NormVjp mode) {
     if (need[1]) r[1] = dw;
     return r;
   });
+  if (v.node->op) v.node->norm = std::move(saved);
+  return v;
 }
 
 Var layer_norm(const Var& x, const std::optional<Var>& w, const std::optional<Var>& b, float eps, NormVjp mode) {
@@ -418,7 +429,21 @@ Var layer_norm(const Var& x, const std::optional<Var>& w, const std::optional<Va
   const int bi = b ? (int)inputs.size() : -1;
   if (b) inputs.push_back(*b);
   const bool has_w = (bool)w;
-  return Var::op(y, "layer_norm", inputs,
+  auto saved = std::make_shared<NormSaved>();
+  saved->ln = true;
+  saved->x = xc;
+  saved->w = wc;
+  saved->b = bc;
+  saved->has_w = has_w;
+  saved->has_b = (bool)b;
+  saved->mean = mean;
+  saved->rstd = rstd;
+  saved->rows = rows;
+  saved->H = H;
+  saved->mode = (int)mode;
+  saved->wi = wi;
+  saved->bi = bi;
+  Var v = Var::op(y, "layer_norm", inputs,
                  [xc, wc, mean, rstd, rows, H, mode, wi, bi, has_w](const Tensor& g, const std::vector<bool>& need) {
                    Grads r(need.size());
                    const bool ndx = need[0], ndw = wi >= 0 && need[wi], ndb = bi >= 0 && need[bi];
@@ -435,6 +460,34 @@ Var layer_norm(const Var& x, const std::optional<Var>& w, const std::optional<Va
                    if (ndb) r[bi] = db;
                    return r;
                  });
+  if (v.node->op) v.node->norm = std::move(saved);
+  return v;
+}
+
+bool norm_act_vjp(const NormSaved& s, int act, const Tensor& g, const std::vector<bool>& need, Tensor& dy,
+                  Grads& grads) {
+  grads.assign(need.size(), std::nullopt);
+  const bool ndx = need[0], ndw = s.wi >= 0 && need[s.wi], ndb = s.bi >= 0 && need[s.bi];
+  Tensor gc = t_contiguous(g.shape == s.x.shape ? g : t_broadcast_to(g, s.x.shape));
+  Tensor d = Tensor::empty(s.x.shape, Dev::Hip);
+  Tensor dx = ndx ? Tensor::empty(s.x.shape, Dev::Hip) : Tensor();
+  Tensor dw = ndw ? Tensor::empty({s.H}, Dev::Hip) : Tensor();
+  Tensor db = ndb ? Tensor::empty({s.H}, Dev::Hip) : Tensor();
+  const float* w = s.has_w ? s.w.data() : nullptr;
+  const int rc = s.ln ? oxi_layer_norm_act_bwd(s.x.data(), w, s.has_b ? s.b.data() : nullptr, s.mean.data(),
+                                               s.rstd.data(), gc.data(), act, d.data(), ndx ? dx.data() : nullptr,
+                                               ndw ? dw.data() : nullptr, ndb ? db.data() : nullptr, s.rows, s.H,
+                                               s.mode)
+                      : oxi_rms_norm_act_bwd(s.x.data(), w, s.rstd.data(), gc.data(), act, d.data(),
+                                             ndx ? dx.data() : nullptr, ndw ? dw.data() : nullptr, s.rows, s.H,
+                                             s.mode);
+  if (rc == OXI_NOT_IMPLEMENTED) return false;
+  hip_check(rc);
+  dy = d;
+  if (ndx) grads[0] = dx;
+  if (ndw) grads[s.wi] = dw;
+  if (ndb) grads[s.bi] = db;
+  return true;
 }
 
 // ---- fused activations (functional.py:194-204) ----------------------------------------
@@ -446,7 +499,7 @@ Var gelu(const Var& x, int approximate) {
   hip_check(oxi_gelu_fwd(xv.data(), xv.strides.data(), y.data(), y.strides.data(), xv.shape.data(), xv.ndim(),
                          approximate));
   Tensor xs = xv;
-  return Var::op(y, "gelu", {x}, [xs, approximate](const Tensor& g, const std::vector<bool>& need) -> Grads {
+  Var v = Var::op(y, "gelu", {x}, [xs, approximate](const Tensor& g, const std::vector<bool>& need) -> Grads {
     if (!need[0]) return {std::nullopt};
     Tensor gb = g.shape == xs.shape ? g : t_broadcast_to(g, xs.shape);
     Tensor dx = Tensor::empty(xs.shape, Dev::Hip);
@@ -455,6 +508,8 @@ Var gelu(const Var& x, int approximate) {
                            xs.shape.data(), xs.ndim(), approximate));
     return {dx};
   });
+  if (v.node->op) v.node->act = approximate == OXI_GELU_ERF ? OXI_ACT_GELU_ERF : OXI_ACT_GELU_TANH;
+  return v;
 }
 
 Var silu(const Var& x) {
@@ -463,7 +518,7 @@ Var silu(const Var& x) {
   Tensor y = Tensor::empty(xv.shape, Dev::Hip);
   hip_check(oxi_silu_fwd(xv.data(), xv.strides.data(), y.data(), y.strides.data(), xv.shape.data(), xv.ndim()));
   Tensor xs = xv;
-  return Var::op(y, "silu", {x}, [xs](const Tensor& g, const std::vector<bool>& need) -> Grads {
+  Var v = Var::op(y, "silu", {x}, [xs](const Tensor& g, const std::vector<bool>& need) -> Grads {
     if (!need[0]) return {std::nullopt};
     Tensor gb = g.shape == xs.shape ? g : t_broadcast_to(g, xs.shape);
     Tensor dx = Tensor::empty(xs.shape, Dev::Hip);
@@ -472,6 +527,8 @@ Var silu(const Var& x) {
                            xs.shape.data(), xs.ndim()));
     return {dx};
   });
+  if (v.node->op) v.node->act = OXI_ACT_SILU;
+  return v;
 }
 
 // ---- softmax family (functional.py:211-222) ---------------------------------------------

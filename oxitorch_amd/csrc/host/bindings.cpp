@@ -474,6 +474,10 @@ PYBIND11_MODULE(_native, m) {
   });
   m.def("is_grad_enabled", &is_grad_enabled);
   m.def("set_grad_enabled", &set_grad_enabled);
+  m.def("fuse_norm_act", &fuse_norm_act,
+        "Whether backward runs a norm VJP and the VJP of an activation on its output as one pass.");
+  m.def("set_fuse_norm_act", &set_fuse_norm_act, "Turn the fused norm + activation VJP on or off; returns the old value.");
+  m.def("fused_norm_act_passes", &fused_norm_act_passes, "Fused norm + activation VJP passes run in this process.");
   m.def("version", []() { return std::string("0.1.0"); });
   m.def("synchronize", []() { hip_check(oxi_hip_sync()); });
   m.def("memory_stats", []() {

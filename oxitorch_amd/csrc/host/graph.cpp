@@ -1,6 +1,10 @@
 // Autograd graph: restates crates/oxi-autograd/src/graph.rs (Var/Node, the
 // thread-local grad mode, accumulate_grad, unbroadcast, topo_order and
 // backward_ext) over device tensors.
+#include <atomic>
+#include <cstdlib>
+#include <cstring>
+#include <unordered_map>
 #include <unordered_set>
 
 #include "host.h"
@@ -108,7 +112,52 @@ std::vector<Var> topo_order(const Var& root) {
 }
 }  // namespace
 
+namespace {
+// -1: follow OXI_FUSE_NORM_ACT; 0 / 1: set by set_fuse_norm_act
+std::atomic<int> g_fuse_override{-1};
+std::atomic<uint64_t> g_fused_passes{0};
+
+// Takes the node's VJP (a copy when the graph is retained), raising the
+// reference's error when an earlier pass consumed it (graph.rs:405-420).
+Vjp take_vjp(Node& nd, bool retain_graph) {
+  std::lock_guard<std::mutex> lk(nd.mu);
+  if (!nd.vjp) {
+    if (retain_graph) err_invalid("internal: op node reached in backward without a VJP");
+    err_invalid(
+        "trying to backward through the graph a second time (or along an already freed path): pass "
+        "retain_graph=True on the first backward call");
+  }
+  if (retain_graph) return *nd.vjp;
+  Vjp f = std::move(*nd.vjp);
+  nd.vjp.reset();
+  return f;
+}
+}  // namespace
+
+bool fuse_norm_act() {
+  const int o = g_fuse_override.load();
+  if (o >= 0) return o == 1;
+  const char* e = std::getenv("OXI_FUSE_NORM_ACT");
+  return !(e && std::strcmp(e, "0") == 0);
+}
+
+uint64_t fused_norm_act_passes() { return g_fused_passes.load(); }
+
+bool set_fuse_norm_act(bool on) {
+  const bool prev = fuse_norm_act();
+  g_fuse_override.store(on ? 1 : 0);
+  return prev;
+}
+
 // graph.rs:373-438
+//
+// One addition to the reference's loop: when an activation node (gelu, silu)
+// takes a norm node's output and that output feeds no other edge of this
+// graph, the activation's VJP and the norm's run as one pass
+// (oxi_*_norm_act_bwd). The norm output's gradient is still formed and
+// stored, and the norm's input gradients are held until the loop reaches the
+// norm node, so every accumulation happens in the reference's order with the
+// same values.
 void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
   if (!root.requires_grad())
     err_invalid("element 0 of tensors does not require grad and does not have a grad_fn");
@@ -127,6 +176,12 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
       std::lock_guard<std::mutex> lk(n.node->mu);
       n.node->grad.reset();
     }
+  // edges into each node from the nodes of this graph
+  std::unordered_map<const Node*, int> uses;
+  if (fuse_norm_act())
+    for (const Var& n : order)
+      for (const Var& in : n.node->inputs) ++uses[in.node.get()];
+  std::unordered_map<const Node*, std::vector<std::optional<Tensor>>> held;  // norm grads from a fused pass
   root.accumulate_grad(s);
   for (auto it = order.rbegin(); it != order.rend(); ++it) {
     Var& n = *it;
@@ -140,26 +195,35 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
     std::vector<bool> needs;
     for (const Var& in : n.node->inputs) needs.push_back(in.requires_grad());
     std::vector<std::optional<Tensor>> grads;
-    if (retain_graph) {
-      Vjp f;  // a copy: the node keeps its VJP for later passes
-      {
-        std::lock_guard<std::mutex> lk(n.node->mu);
-        if (!n.node->vjp) err_invalid("internal: op node reached in backward without a VJP");
-        f = *n.node->vjp;
-      }
-      grads = f(*up, needs);
+    auto h = held.find(n.node.get());
+    if (h != held.end()) {
+      take_vjp(*n.node, retain_graph);  // computed by the fused pass
+      grads = std::move(h->second);
+      held.erase(h);
     } else {
-      Vjp f;
-      {
-        std::lock_guard<std::mutex> lk(n.node->mu);
-        if (!n.node->vjp)
-          err_invalid(
-              "trying to backward through the graph a second time (or along an already freed path): pass "
-              "retain_graph=True on the first backward call");
-        f = std::move(*n.node->vjp);
-        n.node->vjp.reset();
+      Vjp f = take_vjp(*n.node, retain_graph);
+      bool done = false;
+      if (n.node->act >= 0 && n.node->inputs.size() == 1 && needs[0]) {
+        Node* nn = n.node->inputs[0].node.get();
+        bool norm_vjp = false;
+        if (nn->norm && uses[nn] == 1) {
+          std::lock_guard<std::mutex> lk(nn->mu);
+          norm_vjp = (bool)nn->vjp;
+        }
+        if (norm_vjp) {
+          std::vector<bool> nneeds;
+          for (const Var& in : nn->inputs) nneeds.push_back(in.requires_grad());
+          Tensor dy;
+          std::vector<std::optional<Tensor>> ng;
+          if (aops::norm_act_vjp(*nn->norm, n.node->act, *up, nneeds, dy, ng)) {
+            grads = {dy};
+            held[nn] = std::move(ng);
+            done = true;
+            g_fused_passes.fetch_add(1);
+          }
+        }
       }
-      grads = f(*up, needs);
+      if (!done) grads = f(*up, needs);
     }
     const std::vector<Var> inputs = n.node->inputs;
     for (size_t i = 0; i < inputs.size() && i < grads.size(); ++i) {

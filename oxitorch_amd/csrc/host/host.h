@@ -167,6 +167,17 @@ class Var;
 // returns one optional gradient per input (unset = not needed / none).
 using Vjp = std::function<std::vector<std::optional<Tensor>>(const Tensor& g, const std::vector<bool>& needs)>;
 
+// What a norm node keeps so that its VJP can absorb the VJP of an activation
+// applied to its output (oxi_*_norm_act_bwd).
+struct NormSaved {
+  bool ln = false;
+  Tensor x, w, b, mean, rstd;  // contiguous; w, b unused unless has_w / has_b
+  bool has_w = false, has_b = false;
+  int64_t rows = 0, H = 0;
+  int mode = 0;         // OXI_NORM_VJP_*
+  int wi = -1, bi = -1;  // input slots of w and b, -1 when absent
+};
+
 struct Node {
   Tensor value;
   const char* op = nullptr;
@@ -175,6 +186,8 @@ struct Node {
   std::optional<Vjp> vjp;
   std::optional<Tensor> grad;
   bool requires_grad = false;
+  std::shared_ptr<const NormSaved> norm;  // set on layer_norm / rms_norm nodes
+  int act = -1;                            // OXI_ACT_* on gelu / silu nodes
 };
 
 class Var {
@@ -194,6 +207,11 @@ class Var {
 
 Tensor unbroadcast(const Tensor& g, const Shape& shape);
 void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph);
+// Whether backward runs norm + activation VJPs as one pass (OXI_FUSE_NORM_ACT,
+// default on; the setter overrides the environment and returns the old value).
+bool fuse_norm_act();
+bool set_fuse_norm_act(bool on);
+uint64_t fused_norm_act_passes();  // fused passes run so far in this process
 
 // ---- differentiable ops (crates/oxi-autograd/src/ops.rs) ------------------------
 
@@ -224,6 +242,12 @@ Var masked_select(const Var& x, const Var& mask);
 // Fused hot-path nodes: one graph node and one kernel per direction.
 enum class NormVjp { Ref = OXI_NORM_VJP_REF, Exact = OXI_NORM_VJP_EXACT };
 NormVjp norm_vjp_mode();  // OXI_NORM_VJP=ref|exact (default ref)
+// The fused VJP of act(norm(x)) for upstream g (the activation output's
+// gradient): fills dy (the norm output's gradient) and one gradient per norm
+// input as `need` asks. False, with nothing computed, when the rows do not
+// vectorize; the caller then runs the two VJPs.
+bool norm_act_vjp(const NormSaved& s, int act, const Tensor& g, const std::vector<bool>& need, Tensor& dy,
+                  std::vector<std::optional<Tensor>>& grads);
 Var rms_norm(const Var& x, const Var& w, float eps, NormVjp mode);
 Var layer_norm(const Var& x, const std::optional<Var>& w, const std::optional<Var>& b, float eps, NormVjp mode);
 Var gelu(const Var& x, int approximate);

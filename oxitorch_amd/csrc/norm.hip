@@ -16,7 +16,18 @@
 // (python/oxitorch/nn/functional.py:227-240): mean = sum/H in f32,
 // inv = 1/sqrt(var+eps), y = ((x-mu)*inv)*w + b. Row sums are tree-ordered
 // rather than the reference's sequential strip sum (ops.rs:256-257).
+//
+// Norm + activation VJP: when the norm's output y feeds only an activation
+// (gelu or silu), the backward takes the activation's upstream gradient g,
+// recomputes y from x and the saved statistics with the forward's exact
+// arithmetic (no contraction, same operand order, so y is bit-identical),
+// forms dy = g * act'(y) with the same functor as the activation's own VJP,
+// writes dy (the intermediate's gradient) and continues as the norm VJP.
+// Per row that reads x and g and writes dy and dx: 4 row crossings instead
+// of the 6 of the two separate VJPs (activation: read y, g, write dy; norm:
+// read x, dy, write dx).
 #include "internal.h"
+#include "ops.h"
 #include "rowtile.h"
 
 namespace oxi {
@@ -132,17 +143,30 @@ __global__ __launch_bounds__(BS) void norm_fwd_loop_k(const float* __restrict__ 
 // blocks per CU) when 4 float4s per lane would not fit the registers of 16;
 // wider rows 1 per block.
 template <int TPR, int NV>
-constexpr int bwd_threads() { return TPR == 64 ? (NV <= 3 ? 1024 : 512) : BS; }
+constexpr int bwd_threads() { return TPR == 64 ? (NV <= 3 ? 1024 : 512) : TPR; }
 
-template <int TPR, int NV, int MODE, bool LN, bool NTS>
+// ACT_NONE: g is the norm output's gradient. Otherwise g is the gradient of
+// act(y) and the kernel first forms dy = g * act'(y) (written to dyo if set).
+constexpr int ACT_NONE = -1;
+
+template <int ACT>
+__device__ __forceinline__ float act_vjp(float y, float g) {
+  if constexpr (ACT == OXI_ACT_GELU_TANH) return GeluTanhBwd{}(y, g);
+  else if constexpr (ACT == OXI_ACT_GELU_ERF) return GeluErfBwd{}(y, g);
+  else return SiluBwd{}(y, g);
+}
+
+template <int TPR, int NV, int MODE, bool LN, bool NTS, int ACT>
 __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
+                                                 const float* __restrict__ b,
                                                  const float* __restrict__ mean, const float* __restrict__ rstd,
-                                                 const float* __restrict__ g, float* __restrict__ dx,
+                                                 const float* __restrict__ g, float* __restrict__ dyo,
+                                                 float* __restrict__ dx,
                                                  float* __restrict__ part, int64_t rows, int H) {
   constexpr int NT = bwd_threads<TPR, NV>();
   constexpr int GPB = NT / TPR;
   constexpr int ROWF = TPR * NV * 4;  // floats a group covers
-  __shared__ float lds[2 * (BS / 64)];
+  __shared__ float lds[2 * (NT / 64)];
   __shared__ float comb[GPB > 1 ? GPB * ROWF : 1];
   const int t = threadIdx.x % TPR;
   const int gi = threadIdx.x / TPR;
@@ -150,46 +174,77 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
   const float fH = (float)H;
   const float inv_n = 1.0f / fH;
   const f4* w4 = reinterpret_cast<const f4*>(w);
+  const f4* b4 = reinterpret_cast<const f4*>(b);
   const f4 zero = {0.f, 0.f, 0.f, 0.f};
   f4 pdw[NV], pdb[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) { pdw[k] = zero; pdb[k] = zero; }
 
-  // weights (padding lanes: 0); cached, re-read per row to save registers
+  // Wide rows (TPR > 64) keep the loop-invariant weights (and, for the
+  // activation prologue, biases) in registers: a load inside the row loop is
+  // younger than the next row's prefetch, and the in-order vmcnt wait for it
+  // also waits for the prefetch. One-wave rows run 16 waves to a CU at up to
+  // 128 VGPRs, where those registers cost more than the wait: they re-read
+  // w and b (cached) per row. Padding lanes (c >= h4) are zeroed at use.
+  constexpr bool REG_W = TPR > 64;
+  f4 wr[NV], br[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int cc = min(k * TPR + t, h4 - 1);
+    wr[k] = (REG_W && w) ? w4[cc] : f4{1.f, 1.f, 1.f, 1.f};
+    br[k] = (REG_W && ACT != ACT_NONE && LN && b) ? b4[cc] : zero;
+  }
   auto wv_at = [&](int k) -> f4 {
     const int c = k * TPR + t;
-    return (c < h4) ? (w ? w4[c] : f4{1.f, 1.f, 1.f, 1.f}) : zero;
+    if constexpr (REG_W) return c < h4 ? wr[k] : zero;
+    else return c < h4 ? (w ? w4[c] : f4{1.f, 1.f, 1.f, 1.f}) : zero;
   };
-  // rows are double-buffered: the next row's x, g and statistics are in
-  // flight while the current row is reduced and stored
+
+  // Rows are double-buffered: the next row's x, g and statistics are in
+  // flight while the current row is reduced and stored. For wide rows the
+  // two register sets swap roles every row (the loop is unrolled twice, so
+  // no copies) and every prefetch load issues (row and column clamped in
+  // bounds), so the wait before a row's first use counts exactly the
+  // younger loads.
   const int64_t ngroups = (int64_t)gridDim.x * GPB;
   int64_t row = (int64_t)blockIdx.x * GPB + gi;
   int red = 0;  // reductions so far: consecutive ones use alternate LDS slot sets
-  auto slot = [&]() { return lds + ((red++ & 1) ? BS / 64 : 0); };
-  RowTile<TPR, NV> xt, gt;
-  float inv = 0.f, mu = 0.f;
-  if (row < rows) {
-    xt.load(x + row * H, h4, t);
-    gt.load(g + row * H, h4, t);
-    inv = rstd[row];
-    if constexpr (LN) mu = mean[row];
-  }
-  while (row < rows) {
-    const int64_t nrow = row + ngroups;
-    RowTile<TPR, NV> xn, gn;
-    float ninv = 0.f, nmu = 0.f;
-    if (nrow < rows) {
-      xn.load(x + nrow * H, h4, t);
-      gn.load(g + nrow * H, h4, t);
-      ninv = rstd[nrow];
-      if constexpr (LN) nmu = mean[nrow];
+  auto slot = [&]() { return lds + ((red++ & 1) ? NT / 64 : 0); };
+  auto fetch = [&](RowTile<TPR, NV>& xt, RowTile<TPR, NV>& gt, float& inv, float& mu, int64_t r) {
+    r = r < rows ? r : rows - 1;
+    xt.load_clamped(x + r * H, h4, t);
+    gt.load_clamped(g + r * H, h4, t);
+    inv = rstd[r];
+    if constexpr (LN) mu = mean[r];
+  };
+  auto process = [&](RowTile<TPR, NV>& xt, RowTile<TPR, NV>& gt, const float inv, const float mu, const int64_t r) {
+    if constexpr (ACT != ACT_NONE) {
+      // y as the forward wrote it, then dy = g * act'(y)   (padding lanes: 0)
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if (k * TPR + t < h4) {
+          const int c = k * TPR + t;
+          f4 yv = LN ? (xt.v[k] - mu) * inv : xt.v[k] * inv;
+          if (w) yv = yv * (REG_W ? wr[k] : w4[c]);
+          if (LN && b) yv = yv + (REG_W ? br[k] : b4[c]);
+          const f4 gv = gt.v[k];
+          gt.v[k] = f4{act_vjp<ACT>(yv.x, gv.x), act_vjp<ACT>(yv.y, gv.y), act_vjp<ACT>(yv.z, gv.z),
+                       act_vjp<ACT>(yv.w, gv.w)};
+        } else {
+          gt.v[k] = zero;
+        }
+      }
+      if (dyo) gt.template store<NTS>(dyo + r * H, h4, t);
     }
-    // xhat = (x - mu) * inv ; gw = g * w   (padding lanes stay 0)
+    // xhat = (x - mu) * inv ; gw = g * w   (padding lanes: 0)
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = k * TPR + t;
       f4 xh = LN ? (xt.v[k] - mu) * inv : xt.v[k] * inv;
-      if (c >= h4) xh = zero;
+      if (c >= h4) {
+        xh = zero;
+        gt.v[k] = zero;
+      }
       xt.v[k] = xh;  // xt now holds xhat
       pdw[k] = pdw[k] + gt.v[k] * xh;
       if constexpr (LN) pdb[k] = pdb[k] + gt.v[k];
@@ -224,13 +279,52 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
 #pragma unroll
         for (int k = 0; k < NV; ++k) gt.v[k] = ((gt.v[k] - a) - xt.v[k] * bcoef) * inv;
       }
-      gt.template store<NTS>(dx + row * H, h4, t);
+      gt.template store<NTS>(dx + r * H, h4, t);
     }
-    xt = xn;
-    gt = gn;
-    inv = ninv;
-    mu = nmu;
-    row = nrow;
+  };
+  RowTile<TPR, NV> xa, ga, xb, gb;
+  float ia = 0.f, ma = 0.f, ib = 0.f, mb = 0.f;
+  if constexpr (!REG_W) {
+    RowTile<TPR, NV> xt, gt;
+    float inv = 0.f, mu = 0.f;
+    if (row < rows) {
+      xt.load(x + row * H, h4, t);
+      gt.load(g + row * H, h4, t);
+      inv = rstd[row];
+      if constexpr (LN) mu = mean[row];
+    }
+    while (row < rows) {
+      const int64_t nrow = row + ngroups;
+      RowTile<TPR, NV> xn, gn;
+      float ninv = 0.f, nmu = 0.f;
+      if (nrow < rows) {
+        xn.load(x + nrow * H, h4, t);
+        gn.load(g + nrow * H, h4, t);
+        ninv = rstd[nrow];
+        if constexpr (LN) nmu = mean[nrow];
+      }
+      process(xt, gt, inv, mu, row);
+      xt = xn;
+      gt = gn;
+      inv = ninv;
+      mu = nmu;
+      row = nrow;
+    }
+  } else {
+    // The scheduling barriers keep the current row's first use below the next
+    // row's loads, so its wait leaves those loads in flight.
+    fetch(xa, ga, ia, ma, row);
+    while (row < rows) {
+      fetch(xb, gb, ib, mb, row + ngroups);
+      __builtin_amdgcn_sched_barrier(0);
+      process(xa, ga, ia, ma, row);
+      row += ngroups;
+      if (row >= rows) break;
+      fetch(xa, ga, ia, ma, row + ngroups);
+      __builtin_amdgcn_sched_barrier(0);
+      process(xb, gb, ib, mb, row);
+      row += ngroups;
+    }
   }
   if (!part) return;
   float* pw = part + (int64_t)blockIdx.x * H;
@@ -364,15 +458,19 @@ bool vec_ok(int64_t H, std::initializer_list<const void*> ptrs) {
 // (TPR, NV) of the backward for a vectorized row of h4 float4s; 0 when it
 // does not fit. The backward keeps its rows multi-float4 per lane: it walks
 // rows grid-strided with column partials, and one-wave groups let 16 rows
-// share a block.
+// share a block. Rows past 2048 floats spread over 512 threads: the norm +
+// activation VJP needs 218 VGPRs at 256 x 4 float4s (2 waves per SIMD) and
+// 128 at 512 x 2 (4 waves per SIMD), and the plain VJP runs as fast at either
+// width, so both use the same configuration and their row sums agree bit
+// for bit.
 int pick_bwd_cfg(int64_t h4) {
   if (h4 <= 64) return 641;
   if (h4 <= 128) return 642;
   if (h4 <= 192) return 643;
   if (h4 <= 256) return 644;
   if (h4 <= 512) return 2562;
-  if (h4 <= 1024) return 2564;
-  if (h4 <= 2048) return 2568;
+  if (h4 <= 1024) return 5122;
+  if (h4 <= 2048) return 5124;
   return 0;
 }
 
@@ -409,13 +507,14 @@ int launch_fwd(const float* x, const float* w, const float* b, float* y, float* 
   return check_launch(LN ? "layer_norm_fwd" : "rms_norm_fwd");
 }
 
-template <bool LN, int MODE, bool NTS>
-void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x, const float* w, const float* mean,
-                    const float* rstd, const float* g, float* dx, float* part, int64_t rows, int h) {
+template <bool LN, int MODE, bool NTS, int ACT>
+void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x, const float* w, const float* b,
+                    const float* mean, const float* rstd, const float* g, float* dyo, float* dx, float* part,
+                    int64_t rows, int h) {
 #define OXI_BWD(TPR, NV)                                                                                   \
   case TPR * 10 + NV:                                                                                      \
-    norm_bwd_k<TPR, NV, MODE, LN, NTS><<<dim3((unsigned)nblk), dim3(nt), 0, s>>>(x, w, mean, rstd, g, dx,  \
-                                                                                part, rows, h);            \
+    norm_bwd_k<TPR, NV, MODE, LN, NTS, ACT><<<dim3((unsigned)nblk), dim3(nt), 0, s>>>(                     \
+        x, w, b, mean, rstd, g, dyo, dx, part, rows, h);                                                   \
     break;
   switch (cfg) {
     OXI_BWD(64, 1)
@@ -423,22 +522,25 @@ void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x
     OXI_BWD(64, 3)
     OXI_BWD(64, 4)
     OXI_BWD(256, 2)
-    OXI_BWD(256, 4)
-    OXI_BWD(256, 8)
+    OXI_BWD(512, 2)
+    OXI_BWD(512, 4)
     default:
-      norm_bwd_loop_k<MODE, LN><<<dim3((unsigned)nblk), dim3(BS), 0, s>>>(x, w, mean, rstd, g, dx, part, rows, h);
+      // vectorized shapes only when fused (the entry point checks)
+      if constexpr (ACT == ACT_NONE)
+        norm_bwd_loop_k<MODE, LN><<<dim3((unsigned)nblk), dim3(BS), 0, s>>>(x, w, mean, rstd, g, dx, part, rows, h);
   }
 #undef OXI_BWD
 }
 
-template <bool LN, int MODE>
-int launch_bwd(const float* x, const float* w, const float* mean, const float* rstd, const float* g,
-               float* dx, float* dw, float* db, int64_t rows, int64_t H) {
+template <bool LN, int MODE, int ACT = ACT_NONE>
+int launch_bwd(const float* x, const float* w, const float* b, const float* mean, const float* rstd,
+               const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H) {
   hipStream_t s = stream();
   const bool need_part = dw || (LN && db);
-  const int cfg = vec_ok(H, {x, w, g, dx}) ? pick_bwd_cfg(H / 4) : 0;
+  const int cfg = vec_ok(H, {x, w, b, g, dyo, dx}) ? pick_bwd_cfg(H / 4) : 0;
+  if (ACT != ACT_NONE && cfg == 0) return fail(OXI_OTHER, "norm_act_bwd: internal: unvectorized fused launch");
   const int tpr = cfg ? cfg / 10 : BS;
-  const int nt = tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : BS;  // bwd_threads<TPR, NV>()
+  const int nt = tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : tpr;  // bwd_threads<TPR, NV>()
   const int gpb = nt / tpr;
   // Blocks: enough to fill the chip, few enough that the partial rows stay
   // a small fraction of the row traffic.
@@ -452,8 +554,10 @@ int launch_bwd(const float* x, const float* w, const float* mean, const float* r
   if (need_part && !ws.p) return OXI_OTHER;
   float* part = ws.as<float>();
   const int h = (int)H;
-  if (nt_stores(rows * H * 4)) launch_bwd_cfg<LN, MODE, true>(cfg, s, nblk, nt, x, w, mean, rstd, g, dx, part, rows, h);
-  else launch_bwd_cfg<LN, MODE, false>(cfg, s, nblk, nt, x, w, mean, rstd, g, dx, part, rows, h);
+  if (nt_stores(rows * H * 4))
+    launch_bwd_cfg<LN, MODE, true, ACT>(cfg, s, nblk, nt, x, w, b, mean, rstd, g, dyo, dx, part, rows, h);
+  else
+    launch_bwd_cfg<LN, MODE, false, ACT>(cfg, s, nblk, nt, x, w, b, mean, rstd, g, dyo, dx, part, rows, h);
   int rc = check_launch(LN ? "layer_norm_bwd" : "rms_norm_bwd");
   if (rc != OXI_OK) return rc;
   if (need_part) {
@@ -462,6 +566,32 @@ int launch_bwd(const float* x, const float* w, const float* mean, const float* r
     rc = check_launch("norm_param_grad_finish");
   }
   return rc;
+}
+
+template <bool LN, int MODE>
+int launch_act_bwd(int act, const float* x, const float* w, const float* b, const float* mean, const float* rstd,
+                   const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H) {
+  switch (act) {
+    case OXI_ACT_GELU_TANH:
+      return launch_bwd<LN, MODE, OXI_ACT_GELU_TANH>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+    case OXI_ACT_GELU_ERF:
+      return launch_bwd<LN, MODE, OXI_ACT_GELU_ERF>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+    default:
+      return launch_bwd<LN, MODE, OXI_ACT_SILU>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+  }
+}
+
+// Shared checks of the fused entry points; OXI_OK means "launch".
+int check_act(const char* what, int act, int mode, const float* x, const float* w, const float* b, const float* g,
+              const float* dyo, const float* dx, int64_t rows, int64_t cols) {
+  if (act != OXI_ACT_GELU_TANH && act != OXI_ACT_GELU_ERF && act != OXI_ACT_SILU)
+    return fail(OXI_INVALID_ARGUMENT, "%s: unknown activation %d", what, act);
+  if (mode != OXI_NORM_VJP_REF && mode != OXI_NORM_VJP_EXACT)
+    return fail(OXI_INVALID_ARGUMENT, "%s: unknown VJP mode %d", what, mode);
+  if (rows && cols && !(vec_ok(cols, {x, w, b, g, dyo, dx}) && pick_bwd_cfg(cols / 4)))
+    return fail(OXI_NOT_IMPLEMENTED, "%s: rows of %lld floats at these addresses do not vectorize; run the two VJPs",
+                what, (long long)cols);
+  return OXI_OK;
 }
 
 int check_rows(const char* what, const void* x, const void* y, int64_t rows, int64_t cols) {
@@ -499,8 +629,9 @@ int oxi_rms_norm_bwd(const float* x, const float* w, const float* rstd, const fl
     return OXI_OK;
   }
   return mode == OXI_NORM_VJP_REF
-             ? launch_bwd<false, OXI_NORM_VJP_REF>(x, w, nullptr, rstd, g, dx, dw, nullptr, rows, cols)
-             : launch_bwd<false, OXI_NORM_VJP_EXACT>(x, w, nullptr, rstd, g, dx, dw, nullptr, rows, cols);
+             ? launch_bwd<false, OXI_NORM_VJP_REF>(x, w, nullptr, nullptr, rstd, g, nullptr, dx, dw, nullptr, rows, cols)
+             : launch_bwd<false, OXI_NORM_VJP_EXACT>(x, w, nullptr, nullptr, rstd, g, nullptr, dx, dw, nullptr, rows,
+                                                     cols);
 }
 
 int oxi_layer_norm_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
@@ -526,8 +657,43 @@ int oxi_layer_norm_bwd(const float* x, const float* w, const float* mean, const 
     return rc;
   }
   return mode == OXI_NORM_VJP_REF
-             ? launch_bwd<true, OXI_NORM_VJP_REF>(x, w, mean, rstd, g, dx, dw, db, rows, cols)
-             : launch_bwd<true, OXI_NORM_VJP_EXACT>(x, w, mean, rstd, g, dx, dw, db, rows, cols);
+             ? launch_bwd<true, OXI_NORM_VJP_REF>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols)
+             : launch_bwd<true, OXI_NORM_VJP_EXACT>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols);
+}
+
+int oxi_rms_norm_act_bwd(const float* x, const float* w, const float* rstd, const float* g, int act, float* dy,
+                         float* dx, float* dw, int64_t rows, int64_t cols, int mode) {
+  if (int rc = check_rows("rms_norm_act_bwd", x, g, rows, cols)) return rc;
+  if (!rstd && rows) return fail(OXI_INVALID_ARGUMENT, "rms_norm_act_bwd: rstd must not be NULL");
+  if (int rc = check_act("rms_norm_act_bwd", act, mode, x, w, nullptr, g, dy, dx, rows, cols)) return rc;
+  OXI_CHECK_INIT();
+  if (rows == 0 || cols == 0) {
+    if (dw && cols) return oxi_fill(dw, cols, 0.f);
+    return OXI_OK;
+  }
+  return mode == OXI_NORM_VJP_REF
+             ? launch_act_bwd<false, OXI_NORM_VJP_REF>(act, x, w, nullptr, nullptr, rstd, g, dy, dx, dw, nullptr,
+                                                       rows, cols)
+             : launch_act_bwd<false, OXI_NORM_VJP_EXACT>(act, x, w, nullptr, nullptr, rstd, g, dy, dx, dw, nullptr,
+                                                         rows, cols);
+}
+
+int oxi_layer_norm_act_bwd(const float* x, const float* w, const float* b, const float* mean, const float* rstd,
+                           const float* g, int act, float* dy, float* dx, float* dw, float* db, int64_t rows,
+                           int64_t cols, int mode) {
+  if (int rc = check_rows("layer_norm_act_bwd", x, g, rows, cols)) return rc;
+  if ((!rstd || !mean) && rows) return fail(OXI_INVALID_ARGUMENT, "layer_norm_act_bwd: mean/rstd must not be NULL");
+  if (int rc = check_act("layer_norm_act_bwd", act, mode, x, w, b, g, dy, dx, rows, cols)) return rc;
+  OXI_CHECK_INIT();
+  if (rows == 0 || cols == 0) {
+    int rc = OXI_OK;
+    if (dw && cols) rc = oxi_fill(dw, cols, 0.f);
+    if (!rc && db && cols) rc = oxi_fill(db, cols, 0.f);
+    return rc;
+  }
+  return mode == OXI_NORM_VJP_REF
+             ? launch_act_bwd<true, OXI_NORM_VJP_REF>(act, x, w, b, mean, rstd, g, dy, dx, dw, db, rows, cols)
+             : launch_act_bwd<true, OXI_NORM_VJP_EXACT>(act, x, w, b, mean, rstd, g, dy, dx, dw, db, rows, cols);
 }
 
 }  // extern "C"

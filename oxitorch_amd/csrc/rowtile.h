@@ -77,6 +77,13 @@ struct RowTile {
       v[k] = (c < h4) ? ld_stream(p + c) : f4{0.f, 0.f, 0.f, 0.f};
     }
   }
+  // Every lane loads: lanes past the row (c >= h4) re-read its last float4,
+  // so the loads issue unconditionally; the caller zeroes those lanes at use.
+  __device__ __forceinline__ void load_clamped(const float* __restrict__ row, int h4, int t) {
+    const f4* p = reinterpret_cast<const f4*>(row);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] = ld_stream(p + min(k * TPR + t, h4 - 1));
+  }
   template <bool NT>
   __device__ __forceinline__ void store(float* __restrict__ row, int h4, int t) const {
     f4* p = reinterpret_cast<f4*>(row);

@@ -1,0 +1,249 @@
+"""The fused norm + activation VJP (oxi_layer_norm_act_bwd, oxi_rms_norm_act_bwd)
+and the graph rule that uses it.
+
+The fused pass must give exactly what the two separate VJPs give (the
+activation's VJP on the norm output, then the norm's VJP on that gradient):
+the kernel recomputes the norm output with the forward's arithmetic and uses
+the activation's own VJP functor, so dy, dx, dw and db are compared bit for
+bit with the two-step path, which the kernel parity tests pin to the oracle.
+One case per norm is also checked against the oracle directly.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+ACTS = ["gelu_tanh", "gelu_erf", "silu"]
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def D(hip, a):
+    return hip.DeviceArray.from_numpy(np.ascontiguousarray(a, dtype=np.float32))
+
+
+def _act_bwd(hip, y, g, act):
+    if act == "silu":
+        return hip.silu_bwd(y, g)
+    return hip.gelu_bwd(y, g, "tanh" if act == "gelu_tanh" else "none")
+
+
+def _same(a, b, what):
+    a, b = a.numpy(), b.numpy()
+    assert a.shape == b.shape, what
+    bad = np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))
+    assert bad.size == 0, f"{what}: {bad.size} of {a.size} differ, first at {bad[0]}: {a.flat[bad[0]]} vs {b.flat[bad[0]]}"
+
+
+def _inputs(shape, seed):
+    r = rng(seed)
+    H = shape[-1]
+    x = r.standard_normal(shape, dtype=np.float32)
+    w = (r.standard_normal(H, dtype=np.float32) * 0.02 + 1).astype(np.float32)
+    b = (r.standard_normal(H, dtype=np.float32) * 0.02).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    return x, w, b, g
+
+
+LN_SHAPES = [(512, 4096), (16, 768), (7, 36), (300, 1000), (5, 8192), (33, 256), (1, 4), (2, 3, 512)]
+
+
+@pytest.mark.parametrize("mode", ["ref", "exact"])
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("shape", LN_SHAPES)
+def test_layer_norm_act_bwd_matches_two_vjps(hip, shape, act, mode):
+    say("layer_norm_act_bwd", shape, act, mode)
+    x, w, b, g = _inputs(shape, 11)
+    dx_, dw_, db_, dg = D(hip, x), D(hip, w), D(hip, b), D(hip, g)
+    y, mean, rstd = hip.layer_norm_fwd(dx_, dw_, db_, 1e-5)
+    dy2 = _act_bwd(hip, y, dg, act)
+    dx2, dw2, db2 = hip.layer_norm_bwd(dx_, dw_, mean, rstd, dy2, mode=mode)
+    dy, dx, dw, db = hip.layer_norm_act_bwd(dx_, dw_, db_, mean, rstd, dg, act, mode=mode)
+    _same(dy, dy2, "dy")
+    _same(dx, dx2, "dx")
+    _same(dw, dw2, "dw")
+    _same(db, db2, "db")
+
+
+@pytest.mark.parametrize("mode", ["ref", "exact"])
+@pytest.mark.parametrize("act", ACTS)
+@pytest.mark.parametrize("shape", [(4096, 768), (9, 40), (64, 1000), (3, 8192), (1, 4)])
+def test_rms_norm_act_bwd_matches_two_vjps(hip, shape, act, mode):
+    say("rms_norm_act_bwd", shape, act, mode)
+    x, w, _, g = _inputs(shape, 12)
+    dx_, dw_, dg = D(hip, x), D(hip, w), D(hip, g)
+    y, rstd = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+    dy2 = _act_bwd(hip, y, dg, act)
+    dx2, dw2 = hip.rms_norm_bwd(dx_, dw_, rstd, dy2, mode=mode)
+    dy, dx, dw = hip.rms_norm_act_bwd(dx_, dw_, rstd, dg, act, mode=mode)
+    _same(dy, dy2, "dy")
+    _same(dx, dx2, "dx")
+    _same(dw, dw2, "dw")
+
+
+def test_layer_norm_act_bwd_without_affine_and_partial_outputs(hip):
+    say("layer_norm_act_bwd no affine / NULL outputs")
+    x, _, _, g = _inputs((64, 2048), 13)
+    dx_, dg = D(hip, x), D(hip, g)
+    y, mean, rstd = hip.layer_norm_fwd(dx_, None, None, 1e-5)
+    dy2 = _act_bwd(hip, y, dg, "gelu_erf")
+    dx2, _, db2 = hip.layer_norm_bwd(dx_, None, mean, rstd, dy2, need_dw=False)
+    dy, dx, dw, db = hip.layer_norm_act_bwd(dx_, None, None, mean, rstd, dg, "gelu_erf", need_dw=False)
+    assert dw is None
+    _same(dy, dy2, "dy")
+    _same(dx, dx2, "dx")
+    _same(db, db2, "db")
+    # only the parameter gradient, no dy and no dx
+    _, _, _, db3 = hip.layer_norm_act_bwd(dx_, None, None, mean, rstd, dg, "gelu_erf", need_dy=False,
+                                          need_dx=False, need_dw=False)
+    _same(db3, db2, "db alone")
+
+
+def test_layer_norm_gelu_fused_against_oracle(hip):
+    """C2's arithmetic at a reduced row count, checked against the oracle."""
+    from oracle import closed_form, ref
+    say("layer_norm_act_bwd vs oracle (256, 4096)")
+    x, w, b, g = _inputs((256, 4096), 2)
+    dx_, dw_, db_ = D(hip, x), D(hip, w), D(hip, b)
+    y, mean, rstd = hip.layer_norm_fwd(dx_, dw_, db_, 1e-5)
+    dy, dx, dw, db = hip.layer_norm_act_bwd(dx_, dw_, db_, mean, rstd, D(hip, g), "gelu_erf")
+    h_ref, mu_ref, inv_ref = ref.layer_norm_fwd(x, w, b, 1e-5)
+    dy_np = dy.numpy()
+    assert_close(dy_np, closed_form.gelu_erf_grad(y.numpy()) * g, what="dy")
+    dx_ref, dw_ref, db_ref = ref.layer_norm_bwd(x, w, mu_ref, inv_ref, dy_np)
+    assert_close(dx.numpy(), dx_ref, what="dx")
+    assert_close(dw.numpy(), dw_ref, rtol=1e-4, atol=1e-4, what="dw")
+    assert_close(db.numpy(), db_ref, rtol=1e-4, atol=1e-4, what="db")
+
+
+def test_rms_norm_silu_fused_against_oracle(hip):
+    from oracle import closed_form, ref
+    say("rms_norm_act_bwd vs oracle (512, 768)")
+    x, w, _, g = _inputs((512, 768), 3)
+    dx_, dw_ = D(hip, x), D(hip, w)
+    y, rstd = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+    dy, dx, dw = hip.rms_norm_act_bwd(dx_, dw_, rstd, D(hip, g), "silu")
+    y_ref, inv_ref = ref.rms_norm_fwd(x, w, 1e-6)
+    dy_np = dy.numpy()
+    assert_close(dy_np, closed_form.silu_grad(y.numpy()) * g, what="dy")
+    dx_ref, dw_ref = ref.rms_norm_bwd(x, w, inv_ref, dy_np)
+    assert_close(dx.numpy(), dx_ref, what="dx")
+    assert_close(dw.numpy(), dw_ref, rtol=1e-4, atol=1e-4, what="dw")
+
+
+def test_unvectorized_rows_are_not_implemented(hip):
+    say("layer_norm_act_bwd unvectorized rows")
+    for H in (770, 8196):
+        x, w, b, g = _inputs((3, H), 14)
+        dx_, dw_, db_ = D(hip, x), D(hip, w), D(hip, b)
+        _, mean, rstd = hip.layer_norm_fwd(dx_, dw_, db_, 1e-5)
+        with pytest.raises(NotImplementedError, match="do not vectorize"):
+            hip.layer_norm_act_bwd(dx_, dw_, db_, mean, rstd, D(hip, g), "silu")
+
+
+# ---- the graph rule ------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def ox(hip):
+    import oxitorch_amd
+
+    return oxitorch_amd
+
+
+def _run_graph(ox, native, fuse, build, shape, seed, retain=1):
+    """Builds the graph with `build`, runs backward `retain` + 1 times (the
+    first ones retaining), and returns the leaf grads and the intermediate's."""
+    prev = native.set_fuse_norm_act(fuse)
+    try:
+        x, w, b, g = _inputs(shape, seed)
+        tx = ox.from_numpy(x, True)
+        tw = ox.from_numpy(w, True)
+        tb = ox.from_numpy(b, True)
+        mid, out = build(tx, tw, tb)
+        seed_t = ox.from_numpy(g)
+        for _ in range(retain):
+            out.backward(seed_t, retain_graph=True)
+        out.backward(seed_t)
+        grads = [t.grad.numpy() if t.grad is not None else None for t in (tx, tw, tb, mid)]
+        return grads
+    finally:
+        native.set_fuse_norm_act(prev)
+
+
+def _graph_cases(F):
+    return {
+        "ln_gelu_tanh": lambda x, w, b: (lambda y: (y, F.gelu(y)))(F.layer_norm(x, w, b)),
+        "ln_gelu_erf": lambda x, w, b: (lambda y: (y, F.gelu(y, approximate="none")))(F.layer_norm(x, w, b)),
+        "ln_silu": lambda x, w, b: (lambda y: (y, F.silu(y)))(F.layer_norm(x, w, b)),
+        "rms_silu": lambda x, w, b: (lambda y: (y, F.silu(y)))(F.rms_norm(x, w)),
+        "rms_gelu": lambda x, w, b: (lambda y: (y, F.gelu(y)))(F.rms_norm(x, w)),
+        # y feeds two edges: the rule must not fire
+        "ln_gelu_plus_y": lambda x, w, b: (lambda y: (y, F.gelu(y) + y))(F.layer_norm(x, w, b)),
+    }
+
+
+@pytest.mark.parametrize("shape", [(64, 768), (2, 5, 1024), (16, 4096), (3, 770)])
+@pytest.mark.parametrize("case", ["ln_gelu_tanh", "ln_gelu_erf", "ln_silu", "rms_silu", "rms_gelu",
+                                  "ln_gelu_plus_y"])
+def test_graph_fusion_is_invisible(ox, case, shape):
+    """Leaf gradients and the norm output's gradient are the same bits with and
+    without the fused pass, through two retained backward passes and a final one."""
+    from oxitorch_amd import _native
+    from oxitorch_amd.nn import functional as F
+    say("graph fusion", case, shape)
+    build = _graph_cases(F)[case]
+    before = _native.fused_norm_act_passes()
+    fused = _run_graph(ox, _native, True, build, shape, 21)
+    ran = _native.fused_norm_act_passes() - before
+    plain = _run_graph(ox, _native, False, build, shape, 21)
+    assert _native.fused_norm_act_passes() - before == ran, "fusion ran while switched off"
+    expect = 0 if (case == "ln_gelu_plus_y" or shape[-1] % 4) else 2
+    assert ran == expect, f"fused passes {ran}, expected {expect}"
+    for name, a, b in zip(["x", "w", "b", "y"], fused, plain):
+        if b is None:
+            assert a is None, name
+            continue
+        assert a.shape == b.shape, name
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{case} {shape}: {name}.grad differs"
+
+
+def test_graph_fusion_frees_both_vjps(ox):
+    from oxitorch_amd import _native
+    from oxitorch_amd.nn import functional as F
+    say("graph fusion: second backward")
+    prev = _native.set_fuse_norm_act(True)
+    try:
+        x, w, b, g = _inputs((8, 256), 22)
+        y = F.gelu(F.layer_norm(ox.from_numpy(x, True), ox.from_numpy(w, True), ox.from_numpy(b, True)))
+        y.backward(ox.from_numpy(g))
+        with pytest.raises(ValueError, match="retain_graph"):
+            y.backward(ox.from_numpy(g))
+    finally:
+        _native.set_fuse_norm_act(prev)
+
+
+def test_graph_fusion_only_param_grads(ox):
+    """x without grad: the fused pass computes dw and db (and dy) only."""
+    from oxitorch_amd import _native
+    from oxitorch_amd.nn import functional as F
+    say("graph fusion: x without grad")
+    x, w, b, g = _inputs((32, 512), 23)
+    outs = []
+    for fuse in (True, False):
+        prev = _native.set_fuse_norm_act(fuse)
+        try:
+            tw, tb = ox.from_numpy(w, True), ox.from_numpy(b, True)
+            F.gelu(F.layer_norm(ox.from_numpy(x), tw, tb)).backward(ox.from_numpy(g))
+            outs.append((tw.grad.numpy(), tb.grad.numpy()))
+        finally:
+            _native.set_fuse_norm_act(prev)
+    for a, b_ in zip(*outs):
+        assert np.array_equal(a.view(np.uint32), b_.view(np.uint32))

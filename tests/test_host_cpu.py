@@ -80,6 +80,16 @@ def test_argument_errors_map_to_value_error():
         capi.call("oxi_scatter_rows", None, 1 << 40, 1 << 30, None, 0, None, None)
     with pytest.raises(ValueError, match="grid too large"):
         capi.call("oxi_masked_select_record_bytes", big, 2, ctypes.byref(ctypes.c_int64()))
+    with pytest.raises(ValueError, match="unknown activation"):
+        capi.call("oxi_layer_norm_act_bwd", None, None, None, None, None, None, 7, None, None, None, None, 0, 4, 0)
+    with pytest.raises(ValueError, match="unknown VJP mode"):
+        capi.call("oxi_rms_norm_act_bwd", None, None, None, None, 2, None, None, None, 0, 4, 9)
+    # rows that do not vectorize: the caller is told to run the two VJPs
+    fake = 1 << 20
+    with pytest.raises(NotImplementedError, match="do not vectorize"):
+        capi.call("oxi_rms_norm_act_bwd", fake, None, fake, fake, 2, None, None, None, 1, 770, 0)
+    with pytest.raises(NotImplementedError, match="do not vectorize"):
+        capi.call("oxi_layer_norm_act_bwd", fake, None, None, fake, fake, fake + 4, 1, None, None, None, None, 1, 8, 0)
 
 
 def test_oracle_is_not_imported_by_the_product():
