@@ -51,7 +51,10 @@ MIB = 1 << 20
 TRAFFIC_BYTES = {
     # profiles/pmc_traffic_c1.md: norm_bwd_k + col_finish_k
     "c1": {"rms_norm_bwd": (36.9 + 0.8) * MIB},
-    "c2": {"layer_norm_fwd": 538.2e6, "gelu_erf_fwd": 537.0e6, "gelu_erf_bwd": 805.5e6, "layer_norm_bwd": 840.2e6},
+    # profiles/pmc_traffic_c2.md (layer_norm_bwd: norm_bwd_k + col_finish_k)
+    "c2": {"layer_norm_fwd": 513.3 * MIB, "gelu_erf_fwd": 512.0 * MIB, "gelu_erf_bwd": 768.0 * MIB,
+           "layer_norm_bwd": (787.0 + 16.1) * MIB},
+    "c2f": {"layer_norm_fwd": 513.3 * MIB, "gelu_erf_fwd": 512.0 * MIB, "layer_norm_gelu_bwd": (1044.0 + 16.1) * MIB},
     # profiles/pmc_traffic_c3.md
     "c3": {"cross_entropy_bwd": 2001.6 * MIB},
     # profiles/pmc_traffic_c4.md and pmc_traffic_c5.md: seg_wave_k + seg_fixup_k
