@@ -247,3 +247,24 @@ def test_graph_fusion_only_param_grads(ox):
             _native.set_fuse_norm_act(prev)
     for a, b_ in zip(*outs):
         assert np.array_equal(a.view(np.uint32), b_.view(np.uint32))
+
+
+@pytest.mark.parametrize("vjp", ["ref", "exact"])
+def test_graph_fusion_x_grad_only_and_exact_mode(ox, vjp):
+    """Only x requires grad (no parameter partials), in both VJP modes."""
+    from oxitorch_amd import _native
+    from oxitorch_amd.nn import functional as F
+    say("graph fusion: x grad only", vjp)
+    x, w, b, g = _inputs((48, 2048), 24)
+    outs = []
+    before = _native.fused_norm_act_passes()
+    for fuse in (True, False):
+        prev = _native.set_fuse_norm_act(fuse)
+        try:
+            tx = ox.from_numpy(x, True)
+            F.silu(F.layer_norm(tx, ox.from_numpy(w), ox.from_numpy(b), vjp=vjp)).backward(ox.from_numpy(g))
+            outs.append(tx.grad.numpy())
+        finally:
+            _native.set_fuse_norm_act(prev)
+    assert _native.fused_norm_act_passes() - before == 1
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
