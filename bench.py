@@ -363,6 +363,27 @@ class C5(Workload):
         ]
         return [(k, f, b[k]) for k, f in ops]
 
+    # The graph's default for the chain's tail: softmax over the last dim of
+    # the rms_norm output, which feeds nothing else, so backward runs both VJPs
+    # as one pass (oxi_rms_norm_act_bwd reads r and g, writes dn and dr).
+    fused_what = ("the C5 step with softmax_bwd + rms_norm_bwd as one oxi_rms_norm_act_bwd(OXI_ACT_SOFTMAX) call "
+                  "(the graph's default backward for softmax(rms_norm(r)))")
+
+    def fused_kernels(self):
+        L, c, R, H = self.hip.lib, self.hip.check, self.rows, self.H
+        E4 = R * H * 4
+        out = []
+        for name, fn, nbytes in self.kernels():
+            if name == "softmax_bwd":
+                continue
+            if name == "rms_norm_bwd":
+                out.append(("rms_norm_softmax_bwd", lambda: c(L.oxi_rms_norm_act_bwd(
+                    self.r.ptr, self.rw.ptr, self.rs2.ptr, self.g.ptr, 3, self.dn.ptr, self.dr.ptr, self.drw.ptr,
+                    R, H, 0)), 4 * E4))
+                continue
+            out.append((name, fn, nbytes))
+        return out
+
     def cpu_step(self, ref, lo, hi):
         # the whole chain on the CPU oracle (batch rows lo..hi of 16)
         h = self.host

@@ -78,9 +78,13 @@ enum { OXI_NORM_VJP_REF = 0, OXI_NORM_VJP_EXACT = 1 };
  * the exact 0.5x(1+erf(x/sqrt2)) that the reference lacks. */
 enum { OXI_GELU_TANH = 0, OXI_GELU_ERF = 1 };
 
-/* Activations a norm VJP can absorb (oxi_*_norm_act_bwd). The two GELU values
- * equal OXI_GELU_*. */
-enum { OXI_ACT_GELU_TANH = 0, OXI_ACT_GELU_ERF = 1, OXI_ACT_SILU = 2 };
+/* Activations a norm VJP can absorb (oxi_*_norm_act_bwd): the elementwise
+ * ones (the two GELU values equal OXI_GELU_*) and softmax / log_softmax over
+ * the last dim. */
+enum {
+  OXI_ACT_GELU_TANH = 0, OXI_ACT_GELU_ERF = 1, OXI_ACT_SILU = 2,
+  OXI_ACT_SOFTMAX = 3, OXI_ACT_LOG_SOFTMAX = 4
+};
 
 /* ------------------------------------------------------------------------ */
 /* Runtime: device identity, memory, stream.                                */
@@ -227,14 +231,16 @@ int oxi_layer_norm_bwd(const float* x, const float* w, const float* mean, const 
  * reverse topological order (crates/oxi-autograd/src/graph.rs:398-436: the
  * activation node's VJP accumulates y's gradient, the norm node's VJP reads
  * it). `g` is the gradient of act(y). y is recomputed from x and the saved
- * statistics with the forward's arithmetic; dy = g * act'(y) is the value
- * oxi_gelu_bwd/oxi_silu_bwd write and is stored to `dy` unless NULL (it is
- * y's gradient, which the graph keeps); dx/dw/db are what the matching
- * oxi_*_norm_bwd computes from dy, bit for bit. Each row then crosses HBM four
- * times (read x and g, write dy and dx) instead of six.
+ * statistics with the forward's arithmetic; dy is the value oxi_gelu_bwd /
+ * oxi_silu_bwd (g * act'(y)) or oxi_softmax_bwd / oxi_log_softmax_bwd (on the
+ * softmax of y, recomputed as oxi_*softmax_fwd forms it) write, and is stored
+ * to `dy` unless NULL (it is y's gradient, which the graph keeps); dx/dw/db
+ * are what the matching oxi_*_norm_bwd computes from dy, bit for bit. Each row
+ * then crosses HBM four times (read x and g, write dy and dx) instead of six.
  * Returns OXI_NOT_IMPLEMENTED and writes nothing when a row does not
- * vectorize (cols % 4 != 0, cols > 8192, or a pointer not 16-byte aligned):
- * the caller then runs the two VJPs. */
+ * vectorize (cols % 4 != 0, cols > 8192, or a pointer not 16-byte aligned),
+ * or, for the softmax kinds, when cols > 2048: the caller then runs the two
+ * VJPs. */
 int oxi_rms_norm_act_bwd(const float* x, const float* w, const float* rstd, const float* g, int act,
                          float* dy, float* dx, float* dw, int64_t rows, int64_t cols, int mode);
 int oxi_layer_norm_act_bwd(const float* x, const float* w, const float* b, const float* mean,

@@ -47,7 +47,7 @@ BINARY = ["add", "sub", "mul", "div", "pow", "min", "max", "eq", "ne", "lt", "le
 REDUCE = ["sum", "mean", "max", "min", "argmax", "argmin", "norm"]
 NORM_VJP = {"ref": 0, "exact": 1}
 GELU = {"tanh": 0, "none": 1, "erf": 1}
-ACT = {"gelu_tanh": 0, "gelu_erf": 1, "silu": 2}
+ACT = {"gelu_tanh": 0, "gelu_erf": 1, "silu": 2, "softmax": 3, "log_softmax": 4}
 
 _SIGS = {
     "oxi_hip_init": [c_int],

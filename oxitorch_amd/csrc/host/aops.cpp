@@ -546,15 +546,18 @@ Var softmax(const Var& x, int64_t dim, bool log) {
   Tensor y = Tensor::empty(xv.shape, Dev::Hip);
   hip_check(log ? oxi_log_softmax_fwd(xc.data(), y.data(), outer, len, inner)
                 : oxi_softmax_fwd(xc.data(), y.data(), outer, len, inner));
-  return Var::op(y, log ? "log_softmax" : "softmax", {x},
-                 [y, outer, len, inner, log](const Tensor& g, const std::vector<bool>& need) -> Grads {
-                   if (!need[0]) return {std::nullopt};
-                   Tensor gc = t_contiguous(g.shape == y.shape ? g : t_broadcast_to(g, y.shape));
-                   Tensor dx = Tensor::empty(y.shape, Dev::Hip);
-                   hip_check(log ? oxi_log_softmax_bwd(y.data(), gc.data(), dx.data(), outer, len, inner)
-                                 : oxi_softmax_bwd(y.data(), gc.data(), dx.data(), outer, len, inner));
-                   return {dx};
-                 });
+  Var v = Var::op(y, log ? "log_softmax" : "softmax", {x},
+                  [y, outer, len, inner, log](const Tensor& g, const std::vector<bool>& need) -> Grads {
+                    if (!need[0]) return {std::nullopt};
+                    Tensor gc = t_contiguous(g.shape == y.shape ? g : t_broadcast_to(g, y.shape));
+                    Tensor dx = Tensor::empty(y.shape, Dev::Hip);
+                    hip_check(log ? oxi_log_softmax_bwd(y.data(), gc.data(), dx.data(), outer, len, inner)
+                                  : oxi_softmax_bwd(y.data(), gc.data(), dx.data(), outer, len, inner));
+                    return {dx};
+                  });
+  // over the last dim a norm VJP can absorb it
+  if (v.node->op && inner == 1) v.node->act = log ? OXI_ACT_LOG_SOFTMAX : OXI_ACT_SOFTMAX;
+  return v;
 }
 
 // ---- cross entropy (functional.py:277-293), targets already resolved ------------------------

@@ -146,8 +146,11 @@ template <int TPR, int NV>
 constexpr int bwd_threads() { return TPR == 64 ? (NV <= 3 ? 1024 : 512) : TPR; }
 
 // ACT_NONE: g is the norm output's gradient. Otherwise g is the gradient of
-// act(y) and the kernel first forms dy = g * act'(y) (written to dyo if set).
+// act(y) and the kernel first forms dy (written to dyo if set): g * act'(y)
+// for the elementwise activations, the softmax VJP over the row for
+// OXI_ACT_SOFTMAX / OXI_ACT_LOG_SOFTMAX.
 constexpr int ACT_NONE = -1;
+constexpr bool is_softmax_act(int act) { return act == OXI_ACT_SOFTMAX || act == OXI_ACT_LOG_SOFTMAX; }
 
 template <int ACT>
 __device__ __forceinline__ float act_vjp(float y, float g) {
@@ -218,7 +221,58 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
     if constexpr (LN) mu = mean[r];
   };
   auto process = [&](RowTile<TPR, NV>& xt, RowTile<TPR, NV>& gt, const float inv, const float mu, const int64_t r) {
-    if constexpr (ACT != ACT_NONE) {
+    if constexpr (is_softmax_act(ACT)) {
+      // p = softmax(y) (or log_softmax) as sm_fwd_k forms it over the same
+      // lane layout, then dy = p * (g - sum(g*p)) (log: g - exp(p) * sum(g))
+      // as sm_bwd_k does; padding lanes (c >= h4) hold 0 in g and in exp(y).
+      constexpr bool LOG = ACT == OXI_ACT_LOG_SOFTMAX;
+      f4 pk[NV];
+      float m = NEG_INF;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        pk[k] = zero;
+        const int c = k * TPR + t;
+        if (c < h4) {
+          f4 yv = LN ? (xt.v[k] - mu) * inv : xt.v[k] * inv;
+          if (w) yv = yv * (REG_W ? wr[k] : w4[c]);
+          if (LN && b) yv = yv + (REG_W ? br[k] : b4[c]);
+          pk[k] = yv;
+          m = fmaxf(m, max4(yv));
+        } else {
+          gt.v[k] = zero;
+        }
+      }
+      m = group_max_once<TPR>(m, slot());
+      float s = 0.f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if (k * TPR + t < h4) {
+          const f4 z = pk[k] - m;
+          const f4 e = exp4(z);
+          s += sum4(e);
+          pk[k] = LOG ? z : e;
+        }
+      }
+      s = rsum1<TPR>(s, slot());
+      if constexpr (LOG) {
+        const float L = logf(s);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) pk[k] = pk[k] - L;
+      } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) pk[k] = pk[k] / s;
+      }
+      float sg = 0.f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) sg += LOG ? sum4(gt.v[k]) : sum4(gt.v[k] * pk[k]);
+      sg = rsum1<TPR>(sg, slot());
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if constexpr (LOG) gt.v[k] = gt.v[k] - exp4(pk[k]) * sg;
+        else gt.v[k] = pk[k] * (gt.v[k] - sg);
+      }
+      if (dyo) gt.template store<NTS>(dyo + r * H, h4, t);
+    } else if constexpr (ACT != ACT_NONE) {
       // y as the forward wrote it, then dy = g * act'(y)   (padding lanes: 0)
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
@@ -576,20 +630,28 @@ int launch_act_bwd(int act, const float* x, const float* w, const float* b, cons
       return launch_bwd<LN, MODE, OXI_ACT_GELU_TANH>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
     case OXI_ACT_GELU_ERF:
       return launch_bwd<LN, MODE, OXI_ACT_GELU_ERF>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
-    default:
+    case OXI_ACT_SILU:
       return launch_bwd<LN, MODE, OXI_ACT_SILU>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+    case OXI_ACT_SOFTMAX:
+      return launch_bwd<LN, MODE, OXI_ACT_SOFTMAX>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+    default:
+      return launch_bwd<LN, MODE, OXI_ACT_LOG_SOFTMAX>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
   }
 }
 
 // Shared checks of the fused entry points; OXI_OK means "launch".
 int check_act(const char* what, int act, int mode, const float* x, const float* w, const float* b, const float* g,
               const float* dyo, const float* dx, int64_t rows, int64_t cols) {
-  if (act != OXI_ACT_GELU_TANH && act != OXI_ACT_GELU_ERF && act != OXI_ACT_SILU)
+  if (act < OXI_ACT_GELU_TANH || act > OXI_ACT_LOG_SOFTMAX)
     return fail(OXI_INVALID_ARGUMENT, "%s: unknown activation %d", what, act);
   if (mode != OXI_NORM_VJP_REF && mode != OXI_NORM_VJP_EXACT)
     return fail(OXI_INVALID_ARGUMENT, "%s: unknown VJP mode %d", what, mode);
   if (rows && cols && !(vec_ok(cols, {x, w, b, g, dyo, dx}) && pick_bwd_cfg(cols / 4)))
     return fail(OXI_NOT_IMPLEMENTED, "%s: rows of %lld floats at these addresses do not vectorize; run the two VJPs",
+                what, (long long)cols);
+  // the softmax's row sums must follow the softmax kernels' lane layout
+  if (rows && cols && is_softmax_act(act) && pick_bwd_cfg(cols / 4) != pick_row_cfg(cols / 4))
+    return fail(OXI_NOT_IMPLEMENTED, "%s: softmax rows of %lld floats use another lane layout; run the two VJPs",
                 what, (long long)cols);
   return OXI_OK;
 }

@@ -39,6 +39,13 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
   else *p = v;
 }
 
+// Row helpers shared by the softmax kernels and the norm + softmax VJP.
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+__device__ __forceinline__ float max4(const f4& v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
+__device__ __forceinline__ float sum4(const f4& v) { return (v.x + v.y) + (v.z + v.w); }
+__device__ __forceinline__ f4 exp4(const f4& v) { return f4{expf(v.x), expf(v.y), expf(v.z), expf(v.w)}; }
+
 // Store hint for a launch writing `bytes` of output: plain between 32 MB and
 // 320 MB, non-temporal otherwise. Measured on MI355X (fwd+bwd steps): plain
 // stores gain 8% on a chain of 50 MB tensors and 1-3% on 268 MB ones, and

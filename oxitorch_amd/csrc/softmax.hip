@@ -23,11 +23,6 @@ namespace oxi {
 namespace {
 
 constexpr int BS = 256;
-constexpr float NEG_INF = -__builtin_huge_valf();
-
-__device__ __forceinline__ float max4(const f4& v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
-__device__ __forceinline__ float sum4(const f4& v) { return (v.x + v.y) + (v.z + v.w); }
-__device__ __forceinline__ f4 exp4(const f4& v) { return f4{expf(v.x), expf(v.y), expf(v.z), expf(v.w)}; }
 
 // Running (max, sum of exp(v - max)) of one thread; `m == -inf` means no
 // finite contribution yet (sum 0).

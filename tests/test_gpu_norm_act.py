@@ -31,6 +31,9 @@ def D(hip, a):
 
 
 def _act_bwd(hip, y, g, act):
+    if act in ("softmax", "log_softmax"):
+        log = act == "log_softmax"
+        return hip.softmax_bwd(hip.softmax_fwd(y, log=log), g, log=log)
     if act == "silu":
         return hip.silu_bwd(y, g)
     return hip.gelu_bwd(y, g, "tanh" if act == "gelu_tanh" else "none")
@@ -87,6 +90,61 @@ def test_rms_norm_act_bwd_matches_two_vjps(hip, shape, act, mode):
     _same(dy, dy2, "dy")
     _same(dx, dx2, "dx")
     _same(dw, dw2, "dw")
+
+
+SOFTMAX_SHAPES = [(512, 768), (64, 1000), (7, 36), (33, 256), (5, 2048), (1, 4), (2, 3, 512)]
+
+
+@pytest.mark.parametrize("norm", ["layer_norm", "rms_norm"])
+@pytest.mark.parametrize("act", ["softmax", "log_softmax"])
+@pytest.mark.parametrize("shape", SOFTMAX_SHAPES)
+def test_norm_softmax_bwd_matches_two_vjps(hip, shape, act, norm):
+    """softmax / log_softmax over the last dim of a norm output: the fused VJP
+    recomputes the softmax as the softmax kernels do, so dy is bit-identical."""
+    say("norm_act_bwd softmax", norm, shape, act)
+    x, w, b, g = _inputs(shape, 15)
+    dx_, dw_, db_, dg = D(hip, x), D(hip, w), D(hip, b), D(hip, g)
+    if norm == "layer_norm":
+        y, mean, rstd = hip.layer_norm_fwd(dx_, dw_, db_, 1e-5)
+        dy2 = _act_bwd(hip, y, dg, act)
+        dx2, dw2, db2 = hip.layer_norm_bwd(dx_, dw_, mean, rstd, dy2)
+        dy, dx, dw, db = hip.layer_norm_act_bwd(dx_, dw_, db_, mean, rstd, dg, act)
+        _same(db, db2, "db")
+    else:
+        y, rstd = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+        dy2 = _act_bwd(hip, y, dg, act)
+        dx2, dw2 = hip.rms_norm_bwd(dx_, dw_, rstd, dy2)
+        dy, dx, dw = hip.rms_norm_act_bwd(dx_, dw_, rstd, dg, act)
+    _same(dy, dy2, "dy")
+    _same(dx, dx2, "dx")
+    _same(dw, dw2, "dw")
+
+
+def test_norm_softmax_against_oracle(hip):
+    """C5's tail, rms_norm -> softmax, at a reduced row count against the oracle."""
+    from oracle import closed_form, ref
+    say("rms_norm_act_bwd softmax vs oracle (256, 768)")
+    x, w, _, g = _inputs((256, 768), 5)
+    dx_, dw_ = D(hip, x), D(hip, w)
+    y, rstd = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+    dy, dx, dw = hip.rms_norm_act_bwd(dx_, dw_, rstd, D(hip, g), "softmax")
+    yy = y.numpy().astype(np.float64)
+    p = np.exp(yy - yy.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    assert_close(dy.numpy(), p * (g - (g * p).sum(-1, keepdims=True)), what="dy")
+    _, inv_ref = ref.rms_norm_fwd(x, w, 1e-6)
+    dx_ref, dw_ref = ref.rms_norm_bwd(x, w, inv_ref, dy.numpy())
+    assert_close(dx.numpy(), dx_ref, what="dx")
+    assert_close(dw.numpy(), dw_ref, rtol=1e-4, atol=1e-4, what="dw")
+
+
+def test_softmax_rows_past_2048_are_not_implemented(hip):
+    say("norm_act_bwd softmax, 4096-float rows")
+    x, w, b, g = _inputs((3, 4096), 16)
+    dx_, dw_ = D(hip, x), D(hip, w)
+    _, rstd = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+    with pytest.raises(NotImplementedError, match="lane layout"):
+        hip.rms_norm_act_bwd(dx_, dw_, rstd, D(hip, g), "softmax")
 
 
 def test_layer_norm_act_bwd_without_affine_and_partial_outputs(hip):
@@ -185,6 +243,8 @@ def _graph_cases(F):
         "ln_silu": lambda x, w, b: (lambda y: (y, F.silu(y)))(F.layer_norm(x, w, b)),
         "rms_silu": lambda x, w, b: (lambda y: (y, F.silu(y)))(F.rms_norm(x, w)),
         "rms_gelu": lambda x, w, b: (lambda y: (y, F.gelu(y)))(F.rms_norm(x, w)),
+        "rms_softmax": lambda x, w, b: (lambda y: (y, F.softmax(y, -1)))(F.rms_norm(x, w)),
+        "ln_log_softmax": lambda x, w, b: (lambda y: (y, F.log_softmax(y, -1)))(F.layer_norm(x, w, b)),
         # y feeds two edges: the rule must not fire
         "ln_gelu_plus_y": lambda x, w, b: (lambda y: (y, F.gelu(y) + y))(F.layer_norm(x, w, b)),
     }
@@ -192,7 +252,7 @@ def _graph_cases(F):
 
 @pytest.mark.parametrize("shape", [(64, 768), (2, 5, 1024), (16, 4096), (3, 770)])
 @pytest.mark.parametrize("case", ["ln_gelu_tanh", "ln_gelu_erf", "ln_silu", "rms_silu", "rms_gelu",
-                                  "ln_gelu_plus_y"])
+                                  "rms_softmax", "ln_log_softmax", "ln_gelu_plus_y"])
 def test_graph_fusion_is_invisible(ox, case, shape):
     """Leaf gradients and the norm output's gradient are the same bits with and
     without the fused pass, through two retained backward passes and a final one."""
@@ -205,7 +265,8 @@ def test_graph_fusion_is_invisible(ox, case, shape):
     ran = _native.fused_norm_act_passes() - before
     plain = _run_graph(ox, _native, False, build, shape, 21)
     assert _native.fused_norm_act_passes() - before == ran, "fusion ran while switched off"
-    expect = 0 if (case == "ln_gelu_plus_y" or shape[-1] % 4) else 2
+    softmax_too_wide = "softmax" in case and shape[-1] > 2048
+    expect = 0 if (case == "ln_gelu_plus_y" or shape[-1] % 4 or softmax_too_wide) else 2
     assert ran == expect, f"fused passes {ran}, expected {expect}"
     for name, a, b in zip(["x", "w", "b", "y"], fused, plain):
         if b is None:
