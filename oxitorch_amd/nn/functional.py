@@ -74,7 +74,11 @@ def layer_norm(x, weight, bias, eps=1e-5, vjp=None):
 
     `vjp` selects the x-gradient: "ref" (default, or OXI_NORM_VJP) reproduces
     the reference graph, where `.apply("rsqrt")` detaches the inverse std;
-    "exact" is the full derivative."""
+    "exact" is the full derivative.
+
+    When the output feeds only a gelu, silu, or last-dim softmax/log_softmax,
+    backward runs both VJPs as one device pass (the same values, bit for bit;
+    OXI_FUSE_NORM_ACT=0 turns it off)."""
     H = x.shape[-1]
     if _is_vec(weight, H) and _is_vec(bias, H):
         return _native.layer_norm(x, weight, bias, eps, vjp)
