@@ -225,6 +225,27 @@ int oxi_layer_norm_fwd(const float* x, const float* w, const float* b, float* y,
 int oxi_layer_norm_bwd(const float* x, const float* w, const float* mean, const float* rstd,
                        const float* g, float* dx, float* dw, float* db,
                        int64_t rows, int64_t cols, int mode);
+/* Fixed device scratch of oxi_layer_norm_bwd_noalloc, per device, held until
+ * the process ends. */
+#define OXI_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+/* oxi_layer_norm_bwd without any allocation. This entry point has no
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same arguments and results as oxi_layer_norm_bwd (the
+ * same kernels and launch shapes, so the outputs are bit-identical); the
+ * column partials of dw/db (2 x blocks x cols floats, at most 2 x 2 x CUs x
+ * cols) live in a fixed OXI_NOALLOC_SCRATCH_BYTES array in device memory
+ * instead of a workspace: on a 256-CU MI355X that covers rows of up to 4096
+ * floats. Larger sizes are refused with OXI_INVALID_ARGUMENT before anything
+ * is launched, and so is a call before oxi_hip_init (initialisation
+ * allocates). Every call on one device shares the array and leaves it
+ * holding its partials; nothing in it needs to start at zero. Calls from
+ * several host threads are serialised, but calls that overlap on the device
+ * (e.g. a captured graph replayed on another stream while a call runs on the
+ * library stream) race on the array. */
+int oxi_layer_norm_bwd_noalloc(const float* x, const float* w, const float* mean, const float* rstd,
+                               const float* g, float* dx, float* dw, float* db,
+                               int64_t rows, int64_t cols, int mode);
 /* The VJPs of act(norm(x)) in one pass, for a graph where the norm's output y
  * feeds only the activation `act` (OXI_ACT_*). They replace the activation's
  * VJP followed by the norm's, which the reference runs as two graph nodes in

@@ -84,6 +84,7 @@ _SIGS = {
     "oxi_rms_norm_bwd": [vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_layer_norm_fwd": [vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_float],
     "oxi_layer_norm_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
+    "oxi_layer_norm_bwd_noalloc": [vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_rms_norm_act_bwd": [vp, vp, vp, vp, c_int, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_layer_norm_act_bwd": [vp, vp, vp, vp, vp, vp, c_int, vp, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_softmax_fwd": [vp, vp, c_i64, c_i64, c_i64],
@@ -340,6 +341,17 @@ def layer_norm_bwd(x, w, mean, rstd, g, mode="ref", need_dx=True, need_dw=True, 
     call("oxi_layer_norm_bwd", x.ptr, w.ptr if w else None, mean.ptr, rstd.ptr, g.ptr, dx.ptr if dx else None,
          dw.ptr if dw else None, db.ptr if db else None, rows, H, NORM_VJP[mode])
     return dx, dw, db
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # OXI_NOALLOC_SCRATCH_BYTES
+
+
+def layer_norm_bwd_noalloc(x, w, mean, rstd, g, dx, dw, db, mode="ref"):
+    """oxi_layer_norm_bwd_noalloc into caller-provided outputs (DeviceArrays
+    or None); the call itself allocates nothing."""
+    rows, H = _rows(x)
+    call("oxi_layer_norm_bwd_noalloc", x.ptr, w.ptr if w else None, mean.ptr, rstd.ptr, g.ptr,
+         dx.ptr if dx else None, dw.ptr if dw else None, db.ptr if db else None, rows, H, NORM_VJP[mode])
 
 
 def rms_norm_act_bwd(x, w, rstd, g, act, mode="ref", need_dy=True, need_dx=True, need_dw=True):

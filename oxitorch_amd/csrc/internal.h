@@ -19,7 +19,16 @@ int fail_hip(hipError_t err, const char* what);
 // Stream of the initialised device; initialises device 0 on first use.
 // Returns nullptr and sets the error when no device can be initialised.
 bool ensure_init();
+// True once the library is bound to a device (no initialisation here).
+bool initialised();
 hipStream_t stream();
+// Device address of the bound device's OXI_NOALLOC_SCRATCH_BYTES scratch
+// array (from hipGetSymbolAddress at init); nullptr before init. Every call
+// that uses it on one device shares it: callers hold noalloc_mutex() from
+// their first launch that touches it to their last, so calls from several
+// host threads do not interleave on the library stream.
+void* noalloc_scratch();
+std::mutex& noalloc_mutex();
 // A second stream, default priority, for work that overlaps the library
 // stream (e.g. the embedding VJP's id sort queued at forward time). Work on
 // it first waits for an event recorded on the library stream, and the

@@ -586,9 +586,26 @@ void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x
 #undef OXI_BWD
 }
 
+// Bytes of column partials the backward needs for (rows, H): 2 x blocks x H
+// floats, or 0 when neither dw nor db is wanted.
+size_t bwd_part_bytes(bool need_part, int64_t rows, int64_t H, int cfg) {
+  if (!need_part) return 0;
+  const int tpr = cfg ? cfg / 10 : BS;
+  const int nt = tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : tpr;  // bwd_threads<TPR, NV>()
+  int64_t nblk = ceil_div(rows, nt / tpr);
+  const int64_t cap = (int64_t)cu_count() * (nt == 1024 ? 1 : 2);
+  if (nblk > cap) nblk = cap;
+  if (nblk < 1) nblk = 1;
+  return sizeof(float) * 2 * (size_t)nblk * (size_t)H;
+}
+
+// `fixed` (when not null) holds at least bwd_part_bytes() bytes of device
+// memory for the column partials; otherwise they come from the caching
+// allocator.
 template <bool LN, int MODE, int ACT = ACT_NONE>
 int launch_bwd(const float* x, const float* w, const float* b, const float* mean, const float* rstd,
-               const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H) {
+               const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H,
+               void* fixed = nullptr) {
   hipStream_t s = stream();
   const bool need_part = dw || (LN && db);
   const int cfg = vec_ok(H, {x, w, b, g, dyo, dx}) ? pick_bwd_cfg(H / 4) : 0;
@@ -604,9 +621,11 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   if (need_part && nblk > cap) nblk = cap;
   if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
   if (nblk < 1) nblk = 1;
-  Workspace ws(need_part ? sizeof(float) * 2 * (size_t)nblk * (size_t)H : 0);
-  if (need_part && !ws.p) return OXI_OTHER;
-  float* part = ws.as<float>();
+  Workspace ws(need_part && !fixed ? sizeof(float) * 2 * (size_t)nblk * (size_t)H : 0);
+  if (need_part && !fixed && !ws.p) return OXI_OTHER;
+  // no partials without dw/db: the kernel then writes none (its launch shape
+  // may have more blocks than bwd_part_bytes() sizes for)
+  float* part = !need_part ? nullptr : fixed ? static_cast<float*>(fixed) : ws.as<float>();
   const int h = (int)H;
   if (nt_stores(rows * H * 4))
     launch_bwd_cfg<LN, MODE, true, ACT>(cfg, s, nblk, nt, x, w, b, mean, rstd, g, dyo, dx, part, rows, h);
@@ -721,6 +740,39 @@ int oxi_layer_norm_bwd(const float* x, const float* w, const float* mean, const 
   return mode == OXI_NORM_VJP_REF
              ? launch_bwd<true, OXI_NORM_VJP_REF>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols)
              : launch_bwd<true, OXI_NORM_VJP_EXACT>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols);
+}
+
+int oxi_layer_norm_bwd_noalloc(const float* x, const float* w, const float* mean, const float* rstd, const float* g,
+                               float* dx, float* dw, float* db, int64_t rows, int64_t cols, int mode) {
+  if (int rc = check_rows("layer_norm_bwd_noalloc", x, g, rows, cols)) return rc;
+  if ((!rstd || !mean) && rows)
+    return fail(OXI_INVALID_ARGUMENT, "layer_norm_bwd_noalloc: mean/rstd must not be NULL");
+  if (mode != OXI_NORM_VJP_REF && mode != OXI_NORM_VJP_EXACT)
+    return fail(OXI_INVALID_ARGUMENT, "layer_norm_bwd_noalloc: unknown VJP mode %d", mode);
+  // initialisation allocates (streams, flags): it must have happened already
+  if (!initialised())
+    return fail(OXI_INVALID_ARGUMENT, "layer_norm_bwd_noalloc: the library is not initialised; call oxi_hip_init "
+                                      "first (this entry point allocates nothing, initialisation does)");
+  if (rows == 0 || cols == 0) {
+    int rc = OXI_OK;
+    if (dw && cols) rc = oxi_fill(dw, cols, 0.f);
+    if (!rc && db && cols) rc = oxi_fill(db, cols, 0.f);
+    return rc;
+  }
+  const int cfg = vec_ok(cols, {x, w, g, dx}) ? pick_bwd_cfg(cols / 4) : 0;
+  const size_t need = bwd_part_bytes(dw || db, rows, cols, cfg);
+  if (need > (size_t)OXI_NOALLOC_SCRATCH_BYTES)
+    return fail(OXI_INVALID_ARGUMENT,
+                "layer_norm_bwd_noalloc: rows of %lld floats need %zu bytes of scratch for the column partials, "
+                "above the fixed %zu bytes; use oxi_layer_norm_bwd",
+                (long long)cols, need, (size_t)OXI_NOALLOC_SCRATCH_BYTES);
+  void* sp = noalloc_scratch();
+  if (!sp) return fail(OXI_OTHER, "layer_norm_bwd_noalloc: no scratch address for the bound device");
+  std::lock_guard<std::mutex> lk(noalloc_mutex());
+  return mode == OXI_NORM_VJP_REF
+             ? launch_bwd<true, OXI_NORM_VJP_REF>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols, sp)
+             : launch_bwd<true, OXI_NORM_VJP_EXACT>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols,
+                                                    sp);
 }
 
 int oxi_rms_norm_act_bwd(const float* x, const float* w, const float* rstd, const float* g, int act, float* dy,

@@ -23,6 +23,13 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// Device scratch of the allocation-free entry point (oxi_layer_norm_bwd_noalloc):
+// OXI_NOALLOC_SCRATCH_BYTES on every device the library runs on, held until
+// the process ends. In host code `scratch` is only a stand-in for the symbol;
+// its device address comes from hipGetSymbolAddress at init (one per device,
+// kept in Runtime::scratch) and is the only way host code refers to it.
+static __device__ __align__(256) unsigned char scratch[OXI_NOALLOC_SCRATCH_BYTES];
+
 struct Runtime {
   std::mutex mu;
   int device = -1;
@@ -39,6 +46,8 @@ struct Runtime {
   size_t bytes_cached = 0;
   int fail_after = 0;  // debug hook
   std::vector<hipEvent_t> events;  // pooled ordering events, see take_event()
+  std::unordered_map<int, void*> scratch;  // device -> device address of `scratch`
+  std::mutex scratch_mu;  // held by an allocation-free call from its first launch to its last
 };
 
 Runtime& rt() {
@@ -64,6 +73,12 @@ int init_locked(Runtime& r, int device) {
   if (device < 0 || device >= n)
     return fail(OXI_INVALID_ARGUMENT, "device index %d out of range for %d HIP device(s)", device, n);
   if ((e = hipSetDevice(device)) != hipSuccess) return fail_hip(e, "hipSetDevice");
+  if (!r.scratch.count(device)) {
+    void* sp = nullptr;
+    if ((e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch))) != hipSuccess || !sp)
+      return fail_hip(e == hipSuccess ? hipErrorInvalidSymbol : e, "hipGetSymbolAddress(scratch)");
+    r.scratch[device] = sp;
+  }
   hipDeviceProp_t prop;
   if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
     return fail_hip(e, "hipGetDeviceProperties");
@@ -104,6 +119,21 @@ int fail(int code, const char* fmt, ...) {
 int fail_hip(hipError_t err, const char* what) {
   return fail(OXI_OTHER, "%s failed: %s", what, hipGetErrorString(err));
 }
+
+bool initialised() {
+  Runtime& r = rt();
+  std::lock_guard<std::mutex> lk(r.mu);
+  return r.stream != nullptr;
+}
+
+void* noalloc_scratch() {
+  Runtime& r = rt();
+  std::lock_guard<std::mutex> lk(r.mu);
+  auto it = r.scratch.find(r.device);
+  return it == r.scratch.end() ? nullptr : it->second;
+}
+
+std::mutex& noalloc_mutex() { return rt().scratch_mu; }
 
 bool ensure_init() {
   Runtime& r = rt();
