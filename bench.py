@@ -4,26 +4,38 @@
 A "step" is one forward+backward pass of a BASELINE.json config over one batch
 of synthetic, seeded input that is already resident in HBM, driven through the
 liboxihip C-ABI (include/oxihip.h) in the order the host core launches it.
-Default workload: config 2, F.layer_norm(affine) -> exact-erf gelu, fwd+bwd,
-fp32, x (16384, 4096). `--config c1|c3|c4|c5` selects the other configs;
-`--config f2` times device DataLoader batches (the step before the path),
-`--config f3` masked_select and the row scatter (fwd+bwd), `--config c2f` the
-C2 step with the fused layer_norm+gelu VJP the graph uses by default (the
-default C2 line also reports it under "fused_vjp"), and
-`--config f4` one AdamW step over GPT-2 small's 148 parameter tensors (the
-optimizer step after backward).
 
-value = algorithmic bytes per step / wall time per step (GB/s). Algorithmic
-bytes are the per-op minimum (each op reads its inputs once and writes its
-outputs once). Wall time comes from HIP events recorded on the library stream
+The default run (`--config all`) measures all five configs C1-C5 and prints
+one JSON line whose headline (`value`, `ms_per_step`, `roofline`,
+`cpu_baseline`) is C3, the largest config (3.15 GB per step), with a block per
+config under `configs`. `--config c1..c5` runs one config; `f2` (device
+DataLoader batches), `f3` (masked_select + row scatter), `f4` (AdamW over
+GPT-2 small's parameters) and `c2f` (C2 with the fused layer_norm+gelu VJP as
+the main line) time the rows after the path.
+
+value = algorithmic bytes per step / time per step (GB/s). Algorithmic bytes
+are the per-op minimum (each op reads its inputs once and writes its outputs
+once). Time per step comes from HIP events recorded on the library stream
 (the stream every liboxihip kernel runs on) around K back-to-back steps.
 
-roofline: the dominant kernel of the step (largest share of step time): its
-algorithmic bytes / its average launch time (HIP events on the same stream)
-against MI355X's 8 TB/s HBM peak.
-cpu_baseline: the CPU oracle (oracle/refcpu.c, a C restatement of the
-reference CPU path) timed on a bounded sample of the same workload on this
-host, one thread.
+Per config:
+- kernels: each C-ABI call of the step timed alone over back-to-back
+  launches (HIP events around the run of launches), with its algorithmic
+  GB/s;
+- roofline: the dominant call (largest time) against MI355X's 8 TB/s HBM
+  peak; `traffic` is its HBM bytes per call from the committed rocprofv3 PMC
+  summary profiles/pmc_traffic_<config>.md (FETCH_SIZE and WRITE_SIZE runs,
+  scaled by a copy kernel's readings);
+- same_bytes_copy: the step's launch sequence with every call replaced by an
+  identity copy moving the same number of bytes: the practical floor for a
+  step of that many launches and bytes on this GPU;
+- cold_cache: median of 20 steps each timed after a 512 MiB fill;
+- cpu_baseline: the CPU oracle (oracle/refcpu.c, a C restatement of the
+  reference CPU path) on a bounded sample of the same workload on this host;
+- fused_vjp (C2, C5): the step with the norm VJP pass that absorbs the
+  activation / softmax VJP, which is the graph's default for these chains;
+- dropin (C1, C2 fused, C5): the same step through the Python surface
+  (F.* and backward() over the host core's graph), with its host time.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -33,39 +45,39 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
 import numpy as np
 
 PEAK_HBM_GBS = 8000.0
+MIB = 1 << 20
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "achieved HBM GB/s (% of MI355X peak) + rows/s, norm/softmax/embed fwd+bwd"
 
-# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled
-# by the same counters' reading of a 1 GiB copy (FETCH x2.0, WRITE x1.0);
-# the runs and the per-kernel tables are in profiles/pmc_traffic_<config>.md.
-MIB = 1 << 20
-TRAFFIC_BYTES = {
-    # profiles/pmc_traffic_c1.md: norm_bwd_k + col_finish_k
-    "c1": {"rms_norm_bwd": (36.9 + 0.8) * MIB},
-    # profiles/pmc_traffic_c2.md (layer_norm_bwd: norm_bwd_k + col_finish_k)
-    "c2": {"layer_norm_fwd": 513.3 * MIB, "gelu_erf_fwd": 512.0 * MIB, "gelu_erf_bwd": 768.0 * MIB,
-           "layer_norm_bwd": (787.0 + 16.1) * MIB},
-    "c2f": {"layer_norm_fwd": 513.3 * MIB, "gelu_erf_fwd": 512.0 * MIB, "layer_norm_gelu_bwd": (1044.0 + 16.1) * MIB},
-    # profiles/pmc_traffic_c3.md
-    "c3": {"cross_entropy_bwd": 2001.6 * MIB},
-    # profiles/pmc_traffic_c4.md and pmc_traffic_c5.md: seg_wave_k + seg_fixup_k
-    "c4": {"embedding_bwd": (718.5 + 6.6) * MIB},
-    "c5": {"embedding_bwd": (197.4 + 0.0) * MIB},
-    # profiles/pmc_traffic_f3.md: all launches of each C-ABI call
-    "f3": {"masked_select_fwd": 970.8e6, "masked_select_bwd": 425.7e6, "scatter_rows_fwd": 311.2e6,
-           "scatter_rows_bwd": 363.9e6},
-    # profiles/pmc_traffic_f4.md: the 5 launches of one multi-parameter call
-    "f4": {"adamw_step_multi": 3484.9e6},
-}
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def pmc_traffic(config):
+    """HBM bytes per C-ABI call from the committed PMC summary of `config`
+    (its line "traffic per C-ABI call, MiB: name=value; ..."), or {}."""
+    path = os.path.join(PROFILES, f"pmc_traffic_{config}.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return {}
+    m = re.search(r"^traffic per C-ABI call, MiB: (.*)$", text, re.M)
+    if not m:
+        return {}
+    out = {}
+    for item in m.group(1).split(";"):
+        if "=" in item:
+            k, v = item.split("=")
+            out[k.strip()] = float(v) * MIB
+    return out
 
 
 def log(*a):
@@ -77,8 +89,11 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-oracle baseline sample")
+    p.add_argument("--config", default="all", choices=["all"] + sorted(WORKLOADS))
+    p.add_argument("--cpu-seconds", type=float, default=4.0,
+                   help="budget of each config's CPU-oracle baseline sample")
+    p.add_argument("--no-dropin", action="store_true", help="skip the F.*/backward() timing")
+    p.add_argument("--no-cold", action="store_true", help="skip the cold-cache medians")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-copy-probe", action="store_true")
     return p.parse_args()
@@ -122,6 +137,17 @@ class Workload:
     def st(self, vals):
         return self.hip._i64arr(vals)
 
+    def release(self):
+        """Frees the workload's device buffers (the next config reuses the HBM)."""
+        emb = getattr(self, "emb", None)
+        if emb is not None and emb.plan.value:
+            self.hip.check(self.hip.lib.oxi_index_select_bwd_plan_free(emb.plan))
+            emb.plan.value = None
+        for v in list(vars(self).values()):
+            if isinstance(v, self.hip.DeviceArray):
+                v.free()
+        self.hip.sync()
+
 
 # ---------------------------------------------------------------------------
 
@@ -153,6 +179,18 @@ class C1(Workload):
         h = self.host
         y, inv = ref.rms_norm_fwd(h["x"][lo:hi], h["w"], 1e-6)
         ref.rms_norm_bwd(h["x"][lo:hi], h["w"], inv, h["g"][lo:hi])
+
+    dropin_what = "x.grad = w.grad = None; F.rms_norm(x, w, 1e-6).backward(g)"
+
+    def dropin(self, ox, F):
+        h = self.host
+        x, w, g = ox.from_numpy(h["x"], True), ox.from_numpy(h["w"], True), ox.from_numpy(h["g"])
+
+        def step():
+            x.grad = None
+            w.grad = None
+            F.rms_norm(x, w, 1e-6).backward(g)
+        return step
 
 
 class C2(Workload):
@@ -211,6 +249,21 @@ class C2(Workload):
         ref.gelu_erf_fwd(hh)
         dh = ref.gelu_erf_bwd(hh, g)
         ref.layer_norm_bwd(x, h["w"], mu, inv, dh)
+
+    dropin_what = ("x.grad = w.grad = b.grad = None; F.gelu(F.layer_norm(x, w, b, 1e-5), approximate='none')"
+                   ".backward(g) (the graph fuses the two VJPs: compare with fused_vjp)")
+    dropin_vs = "fused_vjp"
+
+    def dropin(self, ox, F):
+        h = self.host
+        x, w, b = (ox.from_numpy(h[k], True) for k in ("x", "w", "b"))
+        g = ox.from_numpy(h["g"])
+
+        def step():
+            for t in (x, w, b):
+                t.grad = None
+            F.gelu(F.layer_norm(x, w, b, 1e-5), approximate="none").backward(g)
+        return step
 
 
 class C2F(C2):
@@ -276,6 +329,10 @@ class C4(Workload):
         self.fwd_bytes = idb + 2 * self.n * Dm * 4
         self.bwd_bytes = idb + self.n * Dm * 4 + V * Dm * 4
         self.bytes_per_step = self.fwd_bytes + self.bwd_bytes
+        # the clipped Zipf ids name few distinct rows: counting each row of W
+        # the gather reads once gives the bytes HBM has to deliver at least
+        self.unique_rows = int(np.unique(ids).size)
+        self.fwd_bytes_unique = idb + self.unique_rows * Dm * 4 + self.n * Dm * 4
 
     def kernels(self):
         L, c = self.hip.lib, self.hip.check
@@ -404,6 +461,27 @@ class C5(Workload):
         dhp = ref.silu_bwd(hp, np.ascontiguousarray(dr.transpose(0, 2, 1)))
         de, _, _ = ref.layer_norm_bwd(e, h["lnw"], mu, inv, np.ascontiguousarray(dhp.transpose(0, 2, 1)))
         ref.index_select_bwd(de.reshape(-1, self.H), h["W"].shape, 0, ids)
+
+    dropin_what = ("leaf grads = None; F.softmax(F.rms_norm(F.silu(F.layer_norm(F.embedding(ids, W).reshape(...), "
+                   "lnw, lnb).permute([0,2,1])).permute([0,2,1]) + pos, rw), -1).backward(g), ids a host list "
+                   "as the reference takes them (the graph fuses the rms_norm + softmax VJPs: compare with "
+                   "fused_vjp)")
+    dropin_vs = "fused_vjp"
+
+    def dropin(self, ox, F):
+        h = self.host
+        B, T, H = self.B, self.T, self.H
+        W, lnw, lnb, rw, pos = (ox.from_numpy(h[k], True) for k in ("W", "lnw", "lnb", "rw", "pos"))
+        g = ox.from_numpy(h["g"])
+        ids = h["ids"].tolist()
+
+        def step():
+            for t in (W, lnw, lnb, rw, pos):
+                t.grad = None
+            e = F.embedding(ids, W).reshape([B, T, H])
+            s = F.silu(F.layer_norm(e, lnw, lnb, 1e-5).permute([0, 2, 1]))
+            F.softmax(F.rms_norm(s.permute([0, 2, 1]) + pos, rw, 1e-6), -1).backward(g)
+        return step
 
 
 def gpt2_small_param_shapes(V=50257, T=1024, H=768, L=12):
@@ -645,18 +723,21 @@ def time_steps(hip, kernels, steps, host=None):
     return ms / steps
 
 
-def time_kernels(hip, kernels, reps):
-    timers = [hip.Timer() for _ in kernels]
-    tot = [0.0] * len(kernels)
-    for _ in range(reps):
-        for i, (_, fn, _) in enumerate(kernels):
-            timers[i].start()
-            fn()
-            tot[i] += timers[i].stop()
+def time_calls(hip, kernels, reps):
+    """Each C-ABI call of the step timed alone: one untimed launch, then
+    `reps` back-to-back launches between two events on the library stream.
+    The average includes no event records between launches."""
+    t = hip.Timer()
     out = {}
-    for i, (label, _, nbytes) in enumerate(kernels):
-        avg = tot[i] / reps
+    for label, fn, nbytes in kernels:
+        fn()
+        hip.sync()
+        t.start()
+        for _ in range(reps):
+            fn()
+        avg = t.stop() / reps
         out[label] = {"ms": avg, "bytes": nbytes, "gbs": nbytes / (avg * 1e-3) / 1e9 if nbytes else None}
+    hip.sync()
     return out
 
 
@@ -676,6 +757,31 @@ def time_cold(hip, kernels, reps=20, flush_bytes=512 << 20):
     scratch.free()
     times.sort()
     return times[len(times) // 2]
+
+
+def same_bytes_copy(hip, kernels, steps):
+    """The step's launch sequence with each call that moves data replaced by
+    one identity copy (oxi_unary IDENTITY, the flat float4 kernel) reading
+    half and writing half of that call's algorithmic bytes: what a step of
+    this many launches and bytes costs when every launch is a plain copy."""
+    sizes = [b for _, _, b in kernels if b > 0]
+    nmax = max(sizes) // 8
+    a, b = hip.DeviceArray((nmax,)), hip.DeviceArray((nmax,))
+    hip.check(hip.lib.oxi_fill(a.ptr, nmax, 1.0))
+    one = hip._i64arr((1,))
+    calls = []
+    for nbytes in sizes:
+        shape = hip._i64arr((nbytes // 8,))
+        calls.append(("copy", lambda shape=shape: hip.check(hip.lib.oxi_unary(19, a.ptr, one, b.ptr, one, shape, 1)),
+                      nbytes))
+    for _ in range(2):
+        for _, fn, _ in calls:
+            fn()
+    ms = time_steps(hip, calls, steps)
+    a.free()
+    b.free()
+    moved = sum(8 * (n // 8) for n in sizes)
+    return {"ms_per_step": round(ms, 5), "gbs": round(moved / (ms * 1e-3) / 1e9, 1), "launches": len(calls)}
 
 
 def copy_probe(hip, nbytes=1 << 30):
@@ -723,7 +829,8 @@ def cpu_threaded(wl, ref, budget_s, threads):
 def cpu_baseline(wl, budget_s):
     from oracle import ref  # the checker/baseline, never the measured product
 
-    if isinstance(wl, (C4, C5)) or getattr(wl, "cpu_full", False):
+    full = isinstance(wl, (C4, C5)) or getattr(wl, "cpu_full", False)
+    if full:
         # a dense dW per call makes row samples unrepresentative (C4, C5), and
         # per-call overhead would swamp small element ranges (F4): time the
         # full workload once
@@ -758,7 +865,7 @@ def cpu_baseline(wl, budget_s):
                   f"(single thread), {el:.2f} s; GB/s scaled by the same algorithmic bytes per row",
     }
     threads = _cpu_threads()
-    if threads > 1 and not (isinstance(wl, (C4, C5)) or getattr(wl, "cpu_full", False)):
+    if threads > 1 and not full:
         # row-parallel like the reference's rayon row reductions (its
         # elementwise passes run on one thread, so this is the faster of the two)
         n, secs = cpu_threaded(wl, ref, budget_s, threads)
@@ -770,6 +877,130 @@ def cpu_baseline(wl, budget_s):
                          f"{n} rows in {secs:.2f} s (single thread: {one['sample']}); GB/s scaled by the same "
                          "algorithmic bytes per row")
     return out
+
+
+def _calls_json(per):
+    return {k: {"avg_ms": round(v["ms"], 5), "gbs": None if v["gbs"] is None else round(v["gbs"], 1)}
+            for k, v in per.items()}
+
+
+def roofline(per, traffic, source):
+    """The dominant call (largest time among the calls that move data)."""
+    dom = max((k for k in per if per[k]["bytes"] > 0), key=lambda k: per[k]["ms"])
+    d = per[dom]
+    return {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(d["gbs"] / PEAK_HBM_GBS, 4), "traffic": traffic.get(dom),
+            "traffic_source": source if dom in traffic else None, "algorithmic_bytes": d["bytes"],
+            "avg_launch_ms": round(d["ms"], 5), "timing": "back-to-back launches of the call alone"}
+
+
+def time_dropin(hip, wl, steps, warmup):
+    """The step through the Python surface (F.* and backward() over the host
+    core's graph): device time per step (events on the library stream around
+    `steps` steps, so host gaps count) and the host's time per step."""
+    import oxitorch_amd as ox
+    from oxitorch_amd.nn import functional as F
+
+    step = wl.dropin(ox, F)
+    for _ in range(max(warmup, 1)):
+        step()
+    hip.sync()
+    t = hip.Timer()
+    t.start()
+    h0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    h1 = time.perf_counter()
+    ms = t.stop() / steps
+    hip.sync()
+    return {"what": wl.dropin_what, "ms_per_step": round(ms, 5), "host_ms_per_step": round((h1 - h0) * 1e3 / steps, 5),
+            "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 2) if not getattr(wl, "dropin_vs", None) else None}
+
+
+def run_config(hip, key, args):
+    """Everything measured for one config; returns its block of the line."""
+    log(f"[{key}] building workload")
+    wl = WORKLOADS[key](hip)
+    kernels = wl.kernels()
+    for _ in range(max(args.warmup, 1)):
+        for _, fn, _ in kernels:
+            fn()
+    hip.sync()
+    log(f"[{key}] timing {args.steps} steps")
+    host_ms = []
+    ms = time_steps(hip, kernels, args.steps, host_ms)
+    reps = max(5, min(args.steps, 20))
+    per = time_calls(hip, kernels, reps)
+    gbs = wl.bytes_per_step / (ms * 1e-3) / 1e9
+    traffic = pmc_traffic(key)
+    block = {
+        "workload": wl.name,
+        "ms_per_step": round(ms, 5),
+        "gbs": round(gbs, 2),
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "rows_per_step": wl.rows,
+        "rows_per_s": round(wl.rows / (ms * 1e-3), 1),
+        "algorithmic_bytes_per_step": wl.bytes_per_step,
+        "host_issue_ms_per_step": round(host_ms[0], 5),
+        "kernels": _calls_json(per),
+        "roofline": roofline(per, traffic, f"profiles/pmc_traffic_{key}.md"),
+    }
+    if isinstance(wl, C4):
+        mu = wl.fwd_bytes_unique + wl.bwd_bytes
+        block["unique_rows"] = {
+            "distinct_ids": wl.unique_rows, "algorithmic_bytes_per_step": mu,
+            "gbs": round(mu / (ms * 1e-3) / 1e9, 2), "pct_of_peak": round(100.0 * mu / (ms * 1e-3) / 1e9 /
+                                                                           PEAK_HBM_GBS, 2),
+            "embedding_fwd_gbs": round(wl.fwd_bytes_unique / (per["embedding_fwd"]["ms"] * 1e-3) / 1e9, 1),
+            "what": "the forward gather counted as reading each distinct row of W once"}
+    if hasattr(wl, "fused_kernels") and not isinstance(wl, C2F):
+        fk = wl.fused_kernels()
+        for _ in range(max(args.warmup, 1)):
+            for _, fn, _ in fk:
+                fn()
+        hip.sync()
+        log(f"[{key}] timing the fused-VJP variant")
+        fms = time_steps(hip, fk, args.steps)
+        fper = time_calls(hip, fk, reps)
+        fbytes = sum(b for _, _, b in fk)
+        block["fused_vjp"] = {
+            "what": wl.fused_what, "ms_per_step": round(fms, 5), "algorithmic_bytes_per_step": fbytes,
+            "gbs": round(fbytes / (fms * 1e-3) / 1e9, 2),
+            "pct_of_peak": round(100.0 * fbytes / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+            "per_op_bytes_gbs": round(wl.bytes_per_step / (fms * 1e-3) / 1e9, 2),
+            "rows_per_s": round(wl.rows / (fms * 1e-3), 1), "kernels": _calls_json(fper)}
+    log(f"[{key}] same-bytes copy floor")
+    block["same_bytes_copy"] = same_bytes_copy(hip, kernels, args.steps)
+    if not args.no_cold:
+        log(f"[{key}] cold-cache median")
+        ms_cold = time_cold(hip, kernels)
+        block["cold_cache"] = {"ms_per_step_median_of_20": round(ms_cold, 5),
+                               "gbs": round(wl.bytes_per_step / (ms_cold * 1e-3) / 1e9, 2),
+                               "protocol": "512 MiB fill before each timed step"}
+    if hasattr(wl, "side_figures"):
+        block["pcie_gbs"] = wl.side_figures()
+    if hasattr(wl, "per_tensor"):
+        alt = wl.per_tensor()
+        ms_alt = time_steps(hip, alt, max(3, min(args.steps, 10)))
+        block["per_tensor_launches"] = {"ms_per_step": round(ms_alt, 5),
+                                        "gbs": round(wl.bytes_per_step / (ms_alt * 1e-3) / 1e9, 2)}
+    if hasattr(wl, "dropin") and not args.no_dropin:
+        log(f"[{key}] timing the F.*/backward() step")
+        d = time_dropin(hip, wl, max(3, min(args.steps, 10)), args.warmup)
+        vs = block.get(getattr(wl, "dropin_vs", None) or "", block)
+        d["vs_capi_ms_per_step"] = vs["ms_per_step"]
+        d["overhead_pct"] = round(100.0 * (d["ms_per_step"] / vs["ms_per_step"] - 1.0), 1)
+        block["dropin"] = d
+    block["cpu_baseline"] = None
+    if not args.no_cpu and args.cpu_seconds > 0:
+        log(f"[{key}] timing the CPU oracle baseline")
+        block["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    wl.release()
+    return block
+
+
+HEADLINE = "c3"
+ALL = ["c1", "c2", "c3", "c4", "c5"]
 
 
 def main():
@@ -784,90 +1015,43 @@ def main():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
     hip.init(0)
-    log(f"building workload {args.config}")
-    wl = WORKLOADS[args.config](hip)
-    kernels = wl.kernels()
-    for _ in range(max(args.warmup, 1)):
-        for _, fn, _ in kernels:
-            fn()
-    hip.sync()
-    log(f"warmup done; timing {args.steps} steps")
-    host_ms = []
-    ms = time_steps(hip, kernels, args.steps, host_ms)
-    per = time_kernels(hip, kernels, max(3, min(args.steps, 10)))
-    # the dominant call among those that move data (the sort plan moves ids
-    # only on the second stream: its main-stream interval is host time)
-    dom = max((k for k in per if per[k]["bytes"] > 0), key=lambda k: per[k]["ms"])
-    d = per[dom]
-    gbs = wl.bytes_per_step / (ms * 1e-3) / 1e9
-    kernel_ms = sum(v["ms"] for v in per.values())
+    keys = ALL if args.config == "all" else [args.config]
+    blocks = {k: run_config(hip, k, args) for k in keys}
+    head_key = HEADLINE if args.config == "all" else args.config
+    head = blocks[head_key]
     line = {
         "metric": METRIC,
-        "value": round(gbs, 2),
+        "value": head["gbs"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded inputs of the config's shapes and distributions)",
-        "config": {"workload": wl.name, "rows_per_step": wl.rows, "algorithmic_bytes_per_step": wl.bytes_per_step},
-        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
-        "rows_per_s": round(wl.rows / (ms * 1e-3), 1),
-        "kernel_ms_per_step": round(kernel_ms, 5),
-        "host_issue_ms_per_step": round(host_ms[0], 5),
-        "kernels": {k: {"avg_ms": round(v["ms"], 5), "gbs": None if v["gbs"] is None else round(v["gbs"], 1)}
-                    for k, v in per.items()},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(d["gbs"] / PEAK_HBM_GBS, 4),
-                     "traffic": TRAFFIC_BYTES.get(args.config, {}).get(dom),
-                     "algorithmic_bytes": d["bytes"]},
-        "cpu_baseline": None,
+        "data": "synthetic (seeded inputs of the configs' shapes and distributions)",
+        "config": {"workload": head["workload"], "headline": head_key,
+                   "why": ("the largest config (3.15 GB per step); every config's block is under configs"
+                           if args.config == "all" else "selected with --config"),
+                   "rows_per_step": head["rows_per_step"],
+                   "algorithmic_bytes_per_step": head["algorithmic_bytes_per_step"]},
+        "pct_of_peak": head["pct_of_peak"],
+        "rows_per_s": head["rows_per_s"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
+        "configs": blocks,
     }
-    if hasattr(wl, "fused_kernels") and not isinstance(wl, C2F):
-        fk = wl.fused_kernels()
-        for _ in range(max(args.warmup, 1)):
-            for _, fn, _ in fk:
-                fn()
-        hip.sync()
-        log("timing the fused-VJP variant")
-        fms = time_steps(hip, fk, args.steps, [])
-        fper = time_kernels(hip, fk, max(3, min(args.steps, 10)))
-        fbytes = sum(b for _, _, b in fk)
-        line["fused_vjp"] = {
-            "what": wl.fused_what, "ms_per_step": round(fms, 5), "algorithmic_bytes_per_step": fbytes,
-            "gbs": round(fbytes / (fms * 1e-3) / 1e9, 2),
-            "pct_of_peak": round(100.0 * fbytes / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
-            "rows_per_s": round(wl.rows / (fms * 1e-3), 1),
-            "kernels": {k: {"avg_ms": round(v["ms"], 5), "gbs": None if v["gbs"] is None else round(v["gbs"], 1)}
-                        for k, v in fper.items()}}
-    log("cold-cache median")
-    ms_cold = time_cold(hip, kernels)
-    line["cold_cache"] = {"ms_per_step_median_of_20": round(ms_cold, 5),
-                          "gbs": round(wl.bytes_per_step / (ms_cold * 1e-3) / 1e9, 2),
-                          "protocol": "512 MiB fill before each timed step"}
     props = hip.device_props()
     # HBM3E moves 4 bits per pin per reported memory clock (8 Gb/s per pin at
     # 2 GHz), so clock x 4 x bus width is the interface peak the props imply
     line["device"] = dict(props, peak_from_props_gbs=round(
         props["memory_clock_khz"] * 1e3 * 4 * props["memory_bus_bits"] / 8 / 1e9, 1),
         peak_datasheet_gbs=PEAK_HBM_GBS)
-    if hasattr(wl, "side_figures"):
-        line["pcie_gbs"] = wl.side_figures()
-    if hasattr(wl, "per_tensor"):
-        alt = wl.per_tensor()
-        ms_alt = time_steps(hip, alt, max(3, min(args.steps, 10)))
-        line["per_tensor_launches"] = {"ms_per_step": round(ms_alt, 5),
-                                       "gbs": round(wl.bytes_per_step / (ms_alt * 1e-3) / 1e9, 2)}
     if not args.no_copy_probe:
         log("copy probe")
         line["stream_copy_gbs"] = copy_probe(hip)
-    if not args.no_cpu and args.cpu_seconds > 0:
-        log("timing CPU oracle baseline")
-        line["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 

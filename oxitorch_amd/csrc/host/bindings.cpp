@@ -321,7 +321,12 @@ PYBIND11_MODULE(_native, m) {
             if (!g) return py::none();
             return py::cast(leaf(*g));
           },
-          [](const PyTensor& s, const PyTensor& g) { s.v.set_grad(g.value()); })
+          // `t.grad = None` clears the gradient (the reference's setter takes a
+          // Tensor only, crates/oxi-bindings/src/lib.rs:354-358)
+          [](const PyTensor& s, const py::object& g) {
+            if (g.is_none()) s.v.clear_grad();
+            else s.v.set_grad(g.cast<PyTensor&>().value());
+          })
       .def("detach", [](const PyTensor& s) { return leaf(s.value()); })
       .def(
           "backward",

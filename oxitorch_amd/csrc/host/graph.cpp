@@ -56,6 +56,11 @@ void Var::set_grad(const Tensor& g) const {  // graph.rs:208-217
   node->grad = g;
 }
 
+void Var::clear_grad() const {
+  std::lock_guard<std::mutex> lk(node->mu);
+  node->grad.reset();
+}
+
 void Var::zero_grad() const {  // graph.rs:229-233
   Tensor z = t_zeros(node->value.shape, node->value.dev());
   std::lock_guard<std::mutex> lk(node->mu);

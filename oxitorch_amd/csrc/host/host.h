@@ -201,6 +201,7 @@ class Var {
   const char* op_name() const { return node->op; }
   std::optional<Tensor> grad() const;
   void set_grad(const Tensor& g) const;
+  void clear_grad() const;  // no gradient (as before the first backward)
   void zero_grad() const;
   void accumulate_grad(const Tensor& g) const;
 };
