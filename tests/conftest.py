@@ -23,6 +23,49 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device; runs the liboxihip kernels")
 
 
+# ---- parity report -------------------------------------------------------------------------
+# The config tests record, per compared quantity, the device's worst error in
+# units of the tolerance (atol + rtol*|want|) against the f32 oracle and
+# against float64, and how many elements only the float64 arbiter admitted.
+# The table is printed at the end of the session and written as JSON lines
+# to $OXI_PARITY_REPORT when set.
+
+PARITY = []
+
+
+def record(config, what, stats):
+    """Adds one compared quantity of `config` to the session's parity report."""
+    PARITY.append(dict(config=config, what=what, **stats))
+    return stats
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not PARITY:
+        return
+    tr = terminalreporter
+    tr.section("parity report (worst error in tolerance units; arbitrated = elements admitted by float64 only)")
+    for r in PARITY:
+        tr.write_line(f"{r['config']:4s} {r['what']:28s} n={r['n']:<11d} vs_oracle={_fmt(r.get('worst_tol'))} "
+                      f"vs_f64={_fmt(r.get('worst_tol_f64'))} ref_vs_f64={_fmt(r.get('ref_worst_tol_f64'))} "
+                      f"arbitrated={r.get('arbitrated', 0)}")
+    path = os.environ.get("OXI_PARITY_REPORT")
+    if path:
+        import json
+        with open(path, "w") as f:
+            for r in PARITY:
+                f.write(json.dumps(r) + "\n")
+
+
+def _fmt(v):
+    return "-" if v is None else f"{v:.3g}"
+
+
+def _worst(got, want, rtol, atol):
+    if got.size == 0:
+        return 0.0
+    return float((np.abs(got - want) / (atol + rtol * np.abs(want))).max())
+
+
 @pytest.fixture(scope="session")
 def hip():
     """The liboxihip ctypes binding with device 0 initialised (fails loudly if absent)."""
@@ -47,6 +90,9 @@ def assert_close(got, want, rtol=RTOL, atol=ATOL, what=""):
             f"{what}: {bad.sum()} of {bad.size} elements outside rtol={rtol} atol={atol}; "
             f"first at flat {i}: got {got.ravel()[i]!r} want {want.ravel()[i]!r}; max err {err.max():.3e}"
         )
+    fin = ~np.isnan(want)
+    return {"n": int(got.size), "worst_tol": float((err[fin] / tol[fin]).max()) if fin.any() else 0.0,
+            "arbitrated": 0}
 
 
 def assert_reduction_close(got, ref32, exact64, rtol=RTOL, atol=ATOL, what=""):
@@ -63,13 +109,16 @@ def assert_reduction_close(got, ref32, exact64, rtol=RTOL, atol=ATOL, what=""):
     tol = atol + rtol * np.abs(exact64)
     e_got = np.abs(got - exact64) / tol
     e_ref = np.abs(ref32 - exact64) / tol
-    worst = e_got.max() if e_got.size else 0.0
+    worst = float(e_got.max()) if e_got.size else 0.0
+    stats = {"n": int(got.size), "worst_tol": _worst(got, ref32, rtol, atol), "worst_tol_f64": worst,
+             "ref_worst_tol_f64": float(e_ref.max()) if e_ref.size else 0.0, "arbitrated": int((e_got > 1.0).sum())}
     if worst <= 1.0:
-        return
+        return stats
     assert worst <= max(1.0, e_ref.max()), (
         f"{what}: device error {worst:.3g} x tolerance exceeds the reference path's own "
         f"worst error {e_ref.max():.3g} x tolerance against the float64 arbiter"
     )
+    return stats
 
 
 def assert_close_arb(got, ref32, exact64, rtol=RTOL, atol=ATOL, what=""):
@@ -90,16 +139,22 @@ def assert_close_arb(got, ref32, exact64, rtol=RTOL, atol=ATOL, what=""):
     assert got.shape == ref32.shape == exact64.shape, f"{what}: shapes differ"
     tol_ex = atol + rtol * np.abs(exact64)
     ok = (np.abs(got - ref32) <= atol + rtol * np.abs(ref32)) | (np.abs(got - exact64) <= tol_ex)
+    e_f64 = np.abs(got - exact64) / tol_ex
+    stats = {"n": int(got.size), "worst_tol": _worst(got, ref32, rtol, atol),
+             "worst_tol_f64": float(e_f64.max()) if e_f64.size else 0.0,
+             "ref_worst_tol_f64": float((np.abs(ref32 - exact64) / tol_ex).max()) if got.size else 0.0,
+             "arbitrated": int((~ok).sum())}
     if ok.all():
-        return
-    worst_got = (np.abs(got - exact64) / tol_ex)[~ok].max()
-    worst_ref = (np.abs(ref32 - exact64) / tol_ex).max()
+        return stats
+    worst_got = e_f64[~ok].max()
+    worst_ref = stats["ref_worst_tol_f64"]
     if worst_got > worst_ref:
         i = np.flatnonzero(~ok.ravel())[0]
         raise AssertionError(
             f"{what}: {(~ok).sum()} of {ok.size} elements outside both tolerances, worst {worst_got:.3g} x tol "
             f"from float64 vs the reference path's worst {worst_ref:.3g} x tol; first at flat {i}: got "
             f"{got.ravel()[i]!r} ref {ref32.ravel()[i]!r} f64 {exact64.ravel()[i]!r}")
+    return stats
 
 
 def assert_sum_close(got, ref32, abs_sum, rtol=RTOL, atol=ATOL, what=""):

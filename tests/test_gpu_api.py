@@ -9,7 +9,7 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import (assert_close, assert_close_arb, assert_reduction_close, assert_sum_close, rng,
+from conftest import (assert_close, assert_close_arb, assert_reduction_close, assert_sum_close, record, rng,
                       segmented_runs_in_one_tile)
 
 pytestmark = pytest.mark.gpu
@@ -389,11 +389,11 @@ def test_config5_gpt2_chain(ox, F):
     y.backward(_t(ox, g))
     y_ref, grads, _ = _c5_oracle(ref, Wa, ids, lnw, lnb, rw, pos, g, ref.softmax_bwd)
     y64, g64 = _c5_f64(Wa, ids, lnw, lnb, rw, pos, g)
-    assert_close_arb(y.numpy(), y_ref, y64, what="C5 y")
+    record("C5", "y", assert_close_arb(y.numpy(), y_ref, y64, what="C5 y"))
     got = dict(W=W.grad.numpy(), lnw=LW.grad.numpy(), lnb=LB.grad.numpy(), rw=RW.grad.numpy(), pos=P.grad.numpy())
     # Ten f32 stages each round differently on the device and in the oracle;
     # where the two differ beyond tolerance the float64 chain arbitrates.
     for k in ("W", "pos"):
-        assert_close_arb(got[k], grads[k], g64[k], what=f"C5 d{k}")
+        record("C5", f"d{k}", assert_close_arb(got[k], grads[k], g64[k], what=f"C5 d{k}"))
     for k in ("lnw", "lnb", "rw"):  # column sums over 16384 rows
-        assert_reduction_close(got[k], grads[k], g64[k], what=f"C5 d{k}")
+        record("C5", f"d{k} (16384-row sums)", assert_reduction_close(got[k], grads[k], g64[k], what=f"C5 d{k}"))

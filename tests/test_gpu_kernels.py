@@ -12,7 +12,7 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import (assert_close, assert_close_arb, assert_reduction_close, rng,
+from conftest import (assert_close, assert_close_arb, assert_reduction_close, record, rng,
                       segmented_runs_in_one_tile)
 
 pytestmark = pytest.mark.gpu
@@ -44,9 +44,13 @@ def test_rms_norm_fwd_bwd_ref(hip, shape):
     assert_close(rstd.numpy(), inv_ref, what="rms rstd")
     dx, dw = hip.rms_norm_bwd(D(hip, x), D(hip, w), rstd, D(hip, g), mode="ref")
     dx_ref, dw_ref = ref.rms_norm_bwd(x, w, inv_ref, g)
-    assert_close(dx.numpy(), dx_ref, what="rms dx(ref)")
+    s_dx = assert_close(dx.numpy(), dx_ref, what="rms dx(ref)")
     _, dw64 = closed_form.rms_norm_bwd_refgraph(x, w, g, 1e-6)
-    assert_reduction_close(dw.numpy(), dw_ref, dw64, what="rms dw")
+    s_dw = assert_reduction_close(dw.numpy(), dw_ref, dw64, what="rms dw")
+    if shape == (4096, 768):  # config 1
+        record("C1", "y", assert_close(y.numpy(), y_ref))
+        record("C1", "dx (ref VJP)", s_dx)
+        record("C1", "dw (4096-row column sums)", s_dw)
 
 
 @pytest.mark.parametrize("shape", [(4096, 768), (9, 40), (5, 3000)])
@@ -122,15 +126,16 @@ def test_layer_norm_c2_full(hip):
     dx, dw, db = hip.layer_norm_bwd(dxx, dw_, mean, rstd, dh, mode="ref")
     h_ref, mu_ref, inv_ref = ref.layer_norm_fwd(x, w, b, 1e-5)
     hh = h.numpy()
-    assert_close(hh, h_ref, what="C2 h")
-    assert_close(y.numpy(), closed_form.gelu_erf(hh), what="C2 gelu(h)")
+    record("C2", "h = layer_norm(x)", assert_close(hh, h_ref, what="C2 h"))
+    record("C2", "gelu(h) vs f64", assert_close(y.numpy(), closed_form.gelu_erf(hh), what="C2 gelu(h)"))
     dh_np = dh.numpy()
-    assert_close(dh_np, closed_form.gelu_erf_grad(hh) * g, what="C2 gelu'(h)*g")
+    record("C2", "dh = gelu'(h) g vs f64", assert_close(dh_np, closed_form.gelu_erf_grad(hh) * g,
+                                                        what="C2 gelu'(h)*g"))
     dx_ref, dw_ref, db_ref = ref.layer_norm_bwd(x, w, mu_ref, inv_ref, dh_np)
-    assert_close(dx.numpy(), dx_ref, what="C2 dx")
+    record("C2", "dx (two VJPs)", assert_close(dx.numpy(), dx_ref, what="C2 dx"))
     _, dw64, db64 = closed_form.layer_norm_bwd_refgraph(x, w, dh_np, 1e-5)
-    assert_reduction_close(dw.numpy(), dw_ref, dw64, what="C2 dw")
-    assert_reduction_close(db.numpy(), db_ref, db64, what="C2 db")
+    record("C2", "dw (16384-row sums)", assert_reduction_close(dw.numpy(), dw_ref, dw64, what="C2 dw"))
+    record("C2", "db (16384-row sums)", assert_reduction_close(db.numpy(), db_ref, db64, what="C2 db"))
 
 
 # ---------------------------------------------------------------------------
@@ -466,6 +471,7 @@ def test_embedding_c4_full(hip):
     dW_, dids = D(hip, W), D(hip, ids)
     out = hip.embedding_fwd(dW_, dids).numpy()
     np.testing.assert_array_equal(out, W[ids])
+    record("C4", "out = W[ids] (bit-exact)", {"n": int(out.size), "worst_tol": 0.0, "arbitrated": 0})
     dg = D(hip, g)
     dW = hip.embedding_bwd(dg, dids, V).numpy()
     dW2 = hip.embedding_bwd(dg, dids, V).numpy()
@@ -475,11 +481,13 @@ def test_embedding_c4_full(hip):
     one = segmented_runs_in_one_tile(ids, V)  # same position-order f32 sum as the reference
     np.testing.assert_array_equal(dW[one], want32[one])
     np.testing.assert_array_equal(dW[counts == 0], 0.0)
+    record("C4", "dW rows of one-tile runs (bit-exact)", {"n": int(dW[one].size), "worst_tol": 0.0, "arbitrated": 0})
     heavy = np.flatnonzero(~one & (counts > 0))
     exact = np.zeros((heavy.size, Dm))
     for j, v in enumerate(heavy):
         exact[j] = g[ids == v].astype(np.float64).sum(0)
-    assert_reduction_close(dW[heavy], want32[heavy], exact, what="C4 heavy dW rows")
+    record("C4", f"dW {heavy.size} multi-tile rows",
+           assert_reduction_close(dW[heavy], want32[heavy], exact, what="C4 heavy dW rows"))
     # conservation: sum over rows of dW equals the sum of all upstream rows
     assert np.allclose(dW.astype(np.float64).sum(0), g.astype(np.float64).sum(0), rtol=1e-5, atol=1e-3)
 
