@@ -9,9 +9,17 @@ The default run (`--config all`) measures all five configs C1-C5 and prints
 one JSON line whose headline (`value`, `ms_per_step`, `roofline`,
 `cpu_baseline`) is C3, the largest config (3.15 GB per step), with a block per
 config under `configs`. `--config c1..c5` runs one config; `f2` (device
-DataLoader batches), `f3` (masked_select + row scatter), `f4` (AdamW over
-GPT-2 small's parameters) and `c2f` (C2 with the fused layer_norm+gelu VJP as
-the main line) time the rows after the path.
+DataLoader batches), `f3` (masked_select + row scatter) and `f4` (AdamW over
+GPT-2 small's parameters) time the rows after the path.
+
+A config's step is the launch sequence the host core runs by default: with
+the graph fusions on, C2's backward is one layer_norm+gelu VJP pass and C5's
+is two fused passes (rms_norm+softmax with the positional gradient,
+layer_norm+silu through the permute). `gbs` divides the metric's per-op
+algorithmic bytes (every F.* op reading its inputs and writing its outputs
+once) by that step's time; `moved_gbs` divides the bytes the default step
+must move. The `unfused` block times the node-by-node sequence (the host
+core with OXI_FUSE_NORM_ACT=0).
 
 value = algorithmic bytes per step / time per step (GB/s). Algorithmic bytes
 are the per-op minimum (each op reads its inputs once and writes its outputs
@@ -32,9 +40,8 @@ Per config:
 - cold_cache: median of 20 steps each timed after a 512 MiB fill;
 - cpu_baseline: the CPU oracle (oracle/refcpu.c, a C restatement of the
   reference CPU path) on a bounded sample of the same workload on this host;
-- fused_vjp (C2, C5): the step with the norm VJP pass that absorbs the
-  activation / softmax VJP, which is the graph's default for these chains;
-- dropin (C1, C2 fused, C5): the same step through the Python surface
+- unfused (C2, C5): the node-by-node step;
+- dropin (C1, C2, C5): the same step through the Python surface
   (F.* and backward() over the host core's graph), with its host time.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
@@ -211,7 +218,7 @@ class C2(Workload):
         self.mean, self.rstd, self.dw, self.db = A((R,)), A((R,)), A((H,)), A((H,))
         self.bytes_per_step = 10 * R * H * 4
 
-    def kernels(self):
+    def unfused_kernels(self):
         L, c, R, H = self.hip.lib, self.hip.check, self.R, self.H
         st, shp = self.st((H, 1)), self.st((R, H))
         E4 = R * H * 4
@@ -225,19 +232,19 @@ class C2(Workload):
                                                               self.dh.ptr, self.dx.ptr, self.dw.ptr, self.db.ptr, R,
                                                               H, 0)), 3 * E4)]
 
-    # The graph's default for this config: when the norm output feeds only the
-    # GELU, backward runs both VJPs as one pass (oxi_layer_norm_act_bwd reads
-    # x and g, writes dy and dx), so a step crosses HBM 8 E-sized times, not
-    # 10. The step above is the path with that fusion off (OXI_FUSE_NORM_ACT=0)
-    # or with other consumers of the norm output; it is the per-op byte count
-    # the metric is defined on.
-    fused_what = ("layer_norm_fwd + gelu_erf_fwd + oxi_layer_norm_act_bwd (the graph's default backward for "
-                  "gelu(layer_norm(x)))")
+    # The host core's default for this config: the norm output feeds only the
+    # GELU, so backward runs both VJPs as one pass (oxi_layer_norm_act_bwd
+    # reads x and g, writes dy and dx) and a step crosses HBM 8 E-sized times
+    # (moved_bytes), not the 10 of the per-op count the metric is defined on.
+    # unfused_kernels() is the path with that fusion off (OXI_FUSE_NORM_ACT=0)
+    # or with other consumers of the norm output.
+    unfused_what = ("layer_norm_fwd + gelu_erf_fwd, then the two VJPs node by node (gelu_erf_bwd, "
+                    "layer_norm_bwd), as the host core runs them with OXI_FUSE_NORM_ACT=0")
 
-    def fused_kernels(self):
+    def kernels(self):
         L, c, R, H = self.hip.lib, self.hip.check, self.R, self.H
         E4 = R * H * 4
-        return C2.kernels(self)[:2] + [
+        return self.unfused_kernels()[:2] + [
             ("layer_norm_gelu_bwd", lambda: c(L.oxi_layer_norm_act_bwd(
                 self.x.ptr, self.w.ptr, self.b.ptr, self.mean.ptr, self.rstd.ptr, self.g.ptr, 1, self.dh.ptr,
                 self.dx.ptr, self.dw.ptr, self.db.ptr, R, H, 0)), 4 * E4)]
@@ -251,8 +258,7 @@ class C2(Workload):
         ref.layer_norm_bwd(x, h["w"], mu, inv, dh)
 
     dropin_what = ("x.grad = w.grad = b.grad = None; F.gelu(F.layer_norm(x, w, b, 1e-5), approximate='none')"
-                   ".backward(g) (the graph fuses the two VJPs: compare with fused_vjp)")
-    dropin_vs = "fused_vjp"
+                   ".backward(g)")
 
     def dropin(self, ox, F):
         h = self.host
@@ -264,19 +270,6 @@ class C2(Workload):
                 t.grad = None
             F.gelu(F.layer_norm(x, w, b, 1e-5), approximate="none").backward(g)
         return step
-
-
-class C2F(C2):
-    """C2 as the graph runs it by default (the norm output feeds only the
-    GELU): the forward kernels of C2, then one pass for both VJPs."""
-
-    def __init__(self, hip):
-        super().__init__(hip)
-        self.name = "C2 layer_norm(affine)+erf-gelu fwd+bwd fp32 x(16384,4096), fused layer_norm+gelu VJP"
-        self.bytes_per_step = 8 * self.R * self.H * 4
-
-    def kernels(self):
-        return self.fused_kernels()
 
 
 class C3(Workload):
@@ -382,8 +375,12 @@ class C5(Workload):
                              pos_grad_reduce=E4 + P4, silu_bwd=3 * E4, layer_norm_bwd=3 * E4,
                              embedding_bwd=ID + E4 + VH4)
         self.bytes_per_step = 26 * E4 + VH4 + 2 * P4 + 2 * ID
+        # the default backward's fused passes: rms_norm + softmax VJP with the
+        # positional gradient (read r, g; write dn, dr, dpos), layer_norm +
+        # silu VJP through the permute (read e, dr; write dh, de)
+        self.op_bytes.update(rms_norm_softmax_pos_bwd=4 * E4 + P4, layer_norm_silu_bwd=4 * E4)
 
-    def kernels(self):
+    def unfused_kernels(self):
         L, c = self.hip.lib, self.hip.check
         V, B, T, H = self.V, self.B, self.T, self.H
         R = B * T
@@ -420,23 +417,30 @@ class C5(Workload):
         ]
         return [(k, f, b[k]) for k, f in ops]
 
-    # The graph's default for the chain's tail: softmax over the last dim of
-    # the rms_norm output, which feeds nothing else, so backward runs both VJPs
-    # as one pass (oxi_rms_norm_act_bwd reads r and g, writes dn and dr).
-    fused_what = ("the C5 step with softmax_bwd + rms_norm_bwd as one oxi_rms_norm_act_bwd(OXI_ACT_SOFTMAX) call "
-                  "(the graph's default backward for softmax(rms_norm(r)))")
+    # The host core's default backward for the chain: softmax over the last
+    # dim of the rms_norm output and the positional table's gradient (the sum
+    # of dr over the batch) in one pass, then silu on the permuted
+    # layer_norm output and the layer_norm VJP in one pass. unfused_kernels()
+    # is the node-by-node order (OXI_FUSE_NORM_ACT=0).
+    unfused_what = ("the chain node by node, as the host core runs it with OXI_FUSE_NORM_ACT=0: softmax_bwd, "
+                    "rms_norm_bwd, the positional gradient as a column sum over the batch, silu_bwd, layer_norm_bwd")
 
-    def fused_kernels(self):
+    def kernels(self):
         L, c, R, H = self.hip.lib, self.hip.check, self.rows, self.H
-        E4 = R * H * 4
+        b = self.op_bytes
         out = []
-        for name, fn, nbytes in self.kernels():
-            if name == "softmax_bwd":
+        for name, fn, nbytes in self.unfused_kernels():
+            if name in ("softmax_bwd", "pos_grad_reduce", "silu_bwd"):
                 continue
             if name == "rms_norm_bwd":
-                out.append(("rms_norm_softmax_bwd", lambda: c(L.oxi_rms_norm_act_bwd(
+                out.append(("rms_norm_softmax_pos_bwd", lambda: c(L.oxi_rms_norm_bwd_lead_sum(
                     self.r.ptr, self.rw.ptr, self.rs2.ptr, self.g.ptr, 3, self.dn.ptr, self.dr.ptr, self.drw.ptr,
-                    R, H, 0)), 4 * E4))
+                    self.dpos.ptr, self.B, R, H, 0)), b["rms_norm_softmax_pos_bwd"]))
+                continue
+            if name == "layer_norm_bwd":
+                out.append(("layer_norm_silu_bwd", lambda: c(L.oxi_layer_norm_act_bwd(
+                    self.e.ptr, self.lnw.ptr, self.lnb.ptr, self.mu.ptr, self.rs1.ptr, self.dr.ptr, 2, self.dh.ptr,
+                    self.de.ptr, self.dlnw.ptr, self.dlnb.ptr, R, H, 0)), b["layer_norm_silu_bwd"]))
                 continue
             out.append((name, fn, nbytes))
         return out
@@ -464,9 +468,7 @@ class C5(Workload):
 
     dropin_what = ("leaf grads = None; F.softmax(F.rms_norm(F.silu(F.layer_norm(F.embedding(ids, W).reshape(...), "
                    "lnw, lnb).permute([0,2,1])).permute([0,2,1]) + pos, rw), -1).backward(g), ids a host list "
-                   "as the reference takes them (the graph fuses the rms_norm + softmax VJPs: compare with "
-                   "fused_vjp)")
-    dropin_vs = "fused_vjp"
+                   "as the reference takes them")
 
     def dropin(self, ox, F):
         h = self.host
@@ -699,7 +701,7 @@ class F3(Workload):
         ref.scatter_dim0_bwd(h["gs"], h["ids"], h["vals"].shape)
 
 
-WORKLOADS = {"c1": C1, "c2": C2, "c2f": C2F, "c3": C3, "c4": C4, "c5": C5, "f2": F2, "f3": F3, "f4": F4}
+WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f2": F2, "f3": F3, "f4": F4}
 
 
 # ---------------------------------------------------------------------------
@@ -914,7 +916,7 @@ def time_dropin(hip, wl, steps, warmup):
     ms = t.stop() / steps
     hip.sync()
     return {"what": wl.dropin_what, "ms_per_step": round(ms, 5), "host_ms_per_step": round((h1 - h0) * 1e3 / steps, 5),
-            "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 2) if not getattr(wl, "dropin_vs", None) else None}
+            "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 2)}
 
 
 def run_config(hip, key, args):
@@ -941,6 +943,9 @@ def run_config(hip, key, args):
         "rows_per_step": wl.rows,
         "rows_per_s": round(wl.rows / (ms * 1e-3), 1),
         "algorithmic_bytes_per_step": wl.bytes_per_step,
+        "launched": "the host core's default launch sequence (graph fusions on); gbs counts the per-op bytes",
+        "moved_bytes_per_step": sum(b for _, _, b in kernels),
+        "moved_gbs": round(sum(b for _, _, b in kernels) / (ms * 1e-3) / 1e9, 2),
         "host_issue_ms_per_step": round(host_ms[0], 5),
         "kernels": _calls_json(per),
         "roofline": roofline(per, traffic, f"profiles/pmc_traffic_{key}.md"),
@@ -953,22 +958,22 @@ def run_config(hip, key, args):
                                                                            PEAK_HBM_GBS, 2),
             "embedding_fwd_gbs": round(wl.fwd_bytes_unique / (per["embedding_fwd"]["ms"] * 1e-3) / 1e9, 1),
             "what": "the forward gather counted as reading each distinct row of W once"}
-    if hasattr(wl, "fused_kernels") and not isinstance(wl, C2F):
-        fk = wl.fused_kernels()
+    if hasattr(wl, "unfused_kernels"):
+        uk = wl.unfused_kernels()
         for _ in range(max(args.warmup, 1)):
-            for _, fn, _ in fk:
+            for _, fn, _ in uk:
                 fn()
         hip.sync()
-        log(f"[{key}] timing the fused-VJP variant")
-        fms = time_steps(hip, fk, args.steps)
-        fper = time_calls(hip, fk, reps)
-        fbytes = sum(b for _, _, b in fk)
-        block["fused_vjp"] = {
-            "what": wl.fused_what, "ms_per_step": round(fms, 5), "algorithmic_bytes_per_step": fbytes,
-            "gbs": round(fbytes / (fms * 1e-3) / 1e9, 2),
-            "pct_of_peak": round(100.0 * fbytes / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
-            "per_op_bytes_gbs": round(wl.bytes_per_step / (fms * 1e-3) / 1e9, 2),
-            "rows_per_s": round(wl.rows / (fms * 1e-3), 1), "kernels": _calls_json(fper)}
+        log(f"[{key}] timing the node-by-node backward")
+        ums = time_steps(hip, uk, args.steps)
+        uper = time_calls(hip, uk, reps)
+        ubytes = sum(b for _, _, b in uk)
+        block["unfused"] = {
+            "what": wl.unfused_what, "ms_per_step": round(ums, 5), "algorithmic_bytes_per_step": ubytes,
+            "gbs": round(ubytes / (ums * 1e-3) / 1e9, 2),
+            "pct_of_peak": round(100.0 * ubytes / (ums * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+            "rows_per_s": round(wl.rows / (ums * 1e-3), 1), "kernels": _calls_json(uper),
+            "roofline": roofline(uper, traffic, f"profiles/pmc_traffic_{key}.md")}
     log(f"[{key}] same-bytes copy floor")
     block["same_bytes_copy"] = same_bytes_copy(hip, kernels, args.steps)
     if not args.no_cold:
@@ -987,9 +992,8 @@ def run_config(hip, key, args):
     if hasattr(wl, "dropin") and not args.no_dropin:
         log(f"[{key}] timing the F.*/backward() step")
         d = time_dropin(hip, wl, max(3, min(args.steps, 10)), args.warmup)
-        vs = block.get(getattr(wl, "dropin_vs", None) or "", block)
-        d["vs_capi_ms_per_step"] = vs["ms_per_step"]
-        d["overhead_pct"] = round(100.0 * (d["ms_per_step"] / vs["ms_per_step"] - 1.0), 1)
+        d["vs_capi_ms_per_step"] = block["ms_per_step"]
+        d["overhead_pct"] = round(100.0 * (d["ms_per_step"] / block["ms_per_step"] - 1.0), 1)
         block["dropin"] = d
     block["cpu_baseline"] = None
     if not args.no_cpu and args.cpu_seconds > 0:

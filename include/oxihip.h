@@ -80,8 +80,10 @@ enum { OXI_GELU_TANH = 0, OXI_GELU_ERF = 1 };
 
 /* Activations a norm VJP can absorb (oxi_*_norm_act_bwd): the elementwise
  * ones (the two GELU values equal OXI_GELU_*) and softmax / log_softmax over
- * the last dim. */
+ * the last dim. OXI_ACT_NONE (the *_lead_sum entry points only) is the plain
+ * norm VJP. */
 enum {
+  OXI_ACT_NONE = -1,
   OXI_ACT_GELU_TANH = 0, OXI_ACT_GELU_ERF = 1, OXI_ACT_SILU = 2,
   OXI_ACT_SOFTMAX = 3, OXI_ACT_LOG_SOFTMAX = 4
 };
@@ -267,6 +269,30 @@ int oxi_rms_norm_act_bwd(const float* x, const float* w, const float* rstd, cons
 int oxi_layer_norm_act_bwd(const float* x, const float* w, const float* b, const float* mean,
                            const float* rstd, const float* g, int act, float* dy, float* dx,
                            float* dw, float* db, int64_t rows, int64_t cols, int mode);
+
+/* The norm VJP (act = OXI_ACT_NONE) or the norm + activation VJP above, over
+ * rows that form a (lead, T) grid (rows = lead * T), that also writes
+ * dx_sum (T, cols): dx_sum[t] = dx[0*T + t] + dx[1*T + t] + ... in batch
+ * order, summed from 0.0f in f32, bit-identical to oxi_reduce(OXI_REDUCE_SUM)
+ * over the leading dim of dx. That is the gradient of a (1, T, cols) operand
+ * broadcast over the leading dim and added to the norm input (a positional
+ * table): the reference forms it after the add's VJP, with unbroadcast
+ * (crates/oxi-autograd/src/graph.rs:274-313, a strided serial column sum,
+ * crates/oxi-tensor/src/lib.rs:549-558), a pass over dx of its own. dy, dx, dw
+ * (and db) are what oxi_*_norm_bwd / oxi_*_norm_act_bwd write, bit for bit;
+ * dx and dx_sum must not be NULL. OXI_NOT_IMPLEMENTED (nothing written) unless
+ * the rows vectorize as oxi_*_norm_act_bwd requires, cols <= 1024 (one wave
+ * per row) and lead is a multiple of 4: the caller then runs the VJP and the
+ * reduction. dw and db
+ * are the column sums the other entry points form, added in another row
+ * order (deterministic, not bit-identical to them). This pass has no
+ * counterpart in the reference. */
+int oxi_rms_norm_bwd_lead_sum(const float* x, const float* w, const float* rstd, const float* g, int act,
+                              float* dy, float* dx, float* dw, float* dx_sum, int64_t lead, int64_t rows,
+                              int64_t cols, int mode);
+int oxi_layer_norm_bwd_lead_sum(const float* x, const float* w, const float* b, const float* mean,
+                                const float* rstd, const float* g, int act, float* dy, float* dx, float* dw,
+                                float* db, float* dx_sum, int64_t lead, int64_t rows, int64_t cols, int mode);
 
 /* ------------------------------------------------------------------------ */
 /* Softmax family over the middle dim of a contiguous (outer, len, inner)    */

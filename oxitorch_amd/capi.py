@@ -47,7 +47,7 @@ BINARY = ["add", "sub", "mul", "div", "pow", "min", "max", "eq", "ne", "lt", "le
 REDUCE = ["sum", "mean", "max", "min", "argmax", "argmin", "norm"]
 NORM_VJP = {"ref": 0, "exact": 1}
 GELU = {"tanh": 0, "none": 1, "erf": 1}
-ACT = {"gelu_tanh": 0, "gelu_erf": 1, "silu": 2, "softmax": 3, "log_softmax": 4}
+ACT = {"none": -1, "gelu_tanh": 0, "gelu_erf": 1, "silu": 2, "softmax": 3, "log_softmax": 4}
 
 _SIGS = {
     "oxi_hip_init": [c_int],
@@ -87,6 +87,8 @@ _SIGS = {
     "oxi_layer_norm_bwd_noalloc": [vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_rms_norm_act_bwd": [vp, vp, vp, vp, c_int, vp, vp, vp, c_i64, c_i64, c_int],
     "oxi_layer_norm_act_bwd": [vp, vp, vp, vp, vp, vp, c_int, vp, vp, vp, vp, c_i64, c_i64, c_int],
+    "oxi_rms_norm_bwd_lead_sum": [vp, vp, vp, vp, c_int, vp, vp, vp, vp, c_i64, c_i64, c_i64, c_int],
+    "oxi_layer_norm_bwd_lead_sum": [vp, vp, vp, vp, vp, vp, c_int, vp, vp, vp, vp, vp, c_i64, c_i64, c_i64, c_int],
     "oxi_softmax_fwd": [vp, vp, c_i64, c_i64, c_i64],
     "oxi_softmax_bwd": [vp, vp, vp, c_i64, c_i64, c_i64],
     "oxi_log_softmax_fwd": [vp, vp, c_i64, c_i64, c_i64],
@@ -341,6 +343,35 @@ def layer_norm_bwd(x, w, mean, rstd, g, mode="ref", need_dx=True, need_dw=True, 
     call("oxi_layer_norm_bwd", x.ptr, w.ptr if w else None, mean.ptr, rstd.ptr, g.ptr, dx.ptr if dx else None,
          dw.ptr if dw else None, db.ptr if db else None, rows, H, NORM_VJP[mode])
     return dx, dw, db
+
+
+def rms_norm_bwd_lead_sum(x, w, rstd, g, lead, act="none", mode="ref", need_dy=True, need_dw=True):
+    """The rms VJP (or rms + act VJP) over (lead, T) rows that also sums dx
+    over the leading dim; returns (dy, dx, dw, dx_sum)."""
+    rows, H = _rows(x)
+    dy = DeviceArray(x.shape) if need_dy and act != "none" else None
+    dx = DeviceArray(x.shape)
+    dw = DeviceArray((H,)) if need_dw else None
+    ds = DeviceArray((rows // lead, H))
+    call("oxi_rms_norm_bwd_lead_sum", x.ptr, w.ptr if w else None, rstd.ptr, g.ptr, ACT[act], dy.ptr if dy else None,
+         dx.ptr, dw.ptr if dw else None, ds.ptr, lead, rows, H, NORM_VJP[mode])
+    return dy, dx, dw, ds
+
+
+def layer_norm_bwd_lead_sum(x, w, b, mean, rstd, g, lead, act="none", mode="ref", need_dy=True, need_dw=True,
+                            need_db=True):
+    """The layer_norm VJP (or layer_norm + act VJP) over (lead, T) rows that
+    also sums dx over the leading dim; returns (dy, dx, dw, db, dx_sum)."""
+    rows, H = _rows(x)
+    dy = DeviceArray(x.shape) if need_dy and act != "none" else None
+    dx = DeviceArray(x.shape)
+    dw = DeviceArray((H,)) if need_dw else None
+    db = DeviceArray((H,)) if need_db else None
+    ds = DeviceArray((rows // lead, H))
+    call("oxi_layer_norm_bwd_lead_sum", x.ptr, w.ptr if w else None, b.ptr if b else None, mean.ptr, rstd.ptr, g.ptr,
+         ACT[act], dy.ptr if dy else None, dx.ptr, dw.ptr if dw else None, db.ptr if db else None, ds.ptr, lead, rows,
+         H, NORM_VJP[mode])
+    return dy, dx, dw, db, ds
 
 
 NOALLOC_SCRATCH_BYTES = 16 << 20  # OXI_NOALLOC_SCRATCH_BYTES

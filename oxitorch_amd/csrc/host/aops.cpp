@@ -231,18 +231,23 @@ Var permute(const Var& x, const std::vector<int64_t>& order) {
   Tensor out = t_permute(x.value(), order);
   std::vector<int64_t> inv(order.size());
   for (size_t i = 0; i < order.size(); ++i) inv[(size_t)normalize_dim(order[i], (int)order.size())] = (int64_t)i;
-  return Var::op(out, "permute", {x}, [inv](const Tensor& g, const std::vector<bool>& need) -> Grads {
+  Var v = Var::op(out, "permute", {x}, [inv](const Tensor& g, const std::vector<bool>& need) -> Grads {
     if (!need[0]) return {std::nullopt};
     return {t_permute(g, inv)};
   });
+  if (v.node->op)
+    for (int64_t o : order) v.node->perm.push_back((int64_t)normalize_dim(o, (int)order.size()));
+  return v;
 }
 
 Var transpose(const Var& x) {
   Tensor out = t_transpose(x.value());
-  return Var::op(out, "transpose", {x}, [](const Tensor& g, const std::vector<bool>& need) -> Grads {
+  Var v = Var::op(out, "transpose", {x}, [](const Tensor& g, const std::vector<bool>& need) -> Grads {
     if (!need[0]) return {std::nullopt};
     return {t_transpose(g)};
   });
+  if (v.node->op) v.node->perm = {1, 0};
+  return v;
 }
 
 Var broadcast_to(const Var& x, const Shape& shape) {
@@ -464,27 +469,40 @@ Var layer_norm(const Var& x, const std::optional<Var>& w, const std::optional<Va
   return v;
 }
 
-bool norm_act_vjp(const NormSaved& s, int act, const Tensor& g, const std::vector<bool>& need, Tensor& dy,
-                  Grads& grads) {
+bool norm_vjp_fused(const NormSaved& s, int act, const Tensor& g, const std::vector<bool>& need, Tensor* dy,
+                    Grads& grads, int64_t lead, Tensor* lsum) {
   grads.assign(need.size(), std::nullopt);
-  const bool ndx = need[0], ndw = s.wi >= 0 && need[s.wi], ndb = s.bi >= 0 && need[s.bi];
+  const bool ndx = need[0] || lsum, ndw = s.wi >= 0 && need[s.wi], ndb = s.bi >= 0 && need[s.bi];
   Tensor gc = t_contiguous(g.shape == s.x.shape ? g : t_broadcast_to(g, s.x.shape));
-  Tensor d = Tensor::empty(s.x.shape, Dev::Hip);
+  Tensor d = act >= 0 ? Tensor::empty(s.x.shape, Dev::Hip) : Tensor();
   Tensor dx = ndx ? Tensor::empty(s.x.shape, Dev::Hip) : Tensor();
   Tensor dw = ndw ? Tensor::empty({s.H}, Dev::Hip) : Tensor();
   Tensor db = ndb ? Tensor::empty({s.H}, Dev::Hip) : Tensor();
+  Tensor ls = lsum ? Tensor::empty({s.rows / lead, s.H}, Dev::Hip) : Tensor();
   const float* w = s.has_w ? s.w.data() : nullptr;
-  const int rc = s.ln ? oxi_layer_norm_act_bwd(s.x.data(), w, s.has_b ? s.b.data() : nullptr, s.mean.data(),
-                                               s.rstd.data(), gc.data(), act, d.data(), ndx ? dx.data() : nullptr,
-                                               ndw ? dw.data() : nullptr, ndb ? db.data() : nullptr, s.rows, s.H,
-                                               s.mode)
-                      : oxi_rms_norm_act_bwd(s.x.data(), w, s.rstd.data(), gc.data(), act, d.data(),
-                                             ndx ? dx.data() : nullptr, ndw ? dw.data() : nullptr, s.rows, s.H,
-                                             s.mode);
+  const float* b = s.has_b ? s.b.data() : nullptr;
+  float* dp = act >= 0 ? d.data() : nullptr;
+  float* dxp = ndx ? dx.data() : nullptr;
+  float* dwp = ndw ? dw.data() : nullptr;
+  float* dbp = ndb ? db.data() : nullptr;
+  int rc;
+  if (lsum)
+    rc = s.ln ? oxi_layer_norm_bwd_lead_sum(s.x.data(), w, b, s.mean.data(), s.rstd.data(), gc.data(), act, dp, dxp,
+                                            dwp, dbp, ls.data(), lead, s.rows, s.H, s.mode)
+              : oxi_rms_norm_bwd_lead_sum(s.x.data(), w, s.rstd.data(), gc.data(), act, dp, dxp, dwp, ls.data(),
+                                          lead, s.rows, s.H, s.mode);
+  else if (act >= 0)
+    rc = s.ln ? oxi_layer_norm_act_bwd(s.x.data(), w, b, s.mean.data(), s.rstd.data(), gc.data(), act, dp, dxp, dwp,
+                                       dbp, s.rows, s.H, s.mode)
+              : oxi_rms_norm_act_bwd(s.x.data(), w, s.rstd.data(), gc.data(), act, dp, dxp, dwp, s.rows, s.H,
+                                     s.mode);
+  else
+    return false;
   if (rc == OXI_NOT_IMPLEMENTED) return false;
   hip_check(rc);
-  dy = d;
-  if (ndx) grads[0] = dx;
+  if (dy) *dy = d;
+  if (lsum) *lsum = ls;
+  if (need[0]) grads[0] = dx;
   if (ndw) grads[s.wi] = dw;
   if (ndb) grads[s.bi] = db;
   return true;

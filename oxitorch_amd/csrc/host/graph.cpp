@@ -154,15 +154,72 @@ bool set_fuse_norm_act(bool on) {
   return prev;
 }
 
+namespace {
+bool has_vjp(Node* nd) {
+  std::lock_guard<std::mutex> lk(nd->mu);
+  return (bool)nd->vjp;
+}
+
+// An add node r = p + q feeding a norm whose input it is, where q is
+// broadcast over the leading dim only ((1, ...) against r's (lead, ...)): the
+// norm pass can also form q's gradient, the sum of dx over that dim, which
+// the add's VJP and unbroadcast would otherwise form in a pass of their own.
+struct LeadSum {
+  Node* add = nullptr;
+  int qi = -1;
+  int64_t lead = 0;
+};
+
+LeadSum lead_sum_of(Node* norm, const std::unordered_map<const Node*, int>& uses) {
+  LeadSum ls;
+  if (norm->inputs.empty()) return ls;
+  Node* a = norm->inputs[0].node.get();
+  auto u = uses.find(a);
+  if (!a->op || std::strcmp(a->op, "add") != 0 || a->inputs.size() != 2 || u == uses.end() || u->second != 1 ||
+      !has_vjp(a))
+    return ls;
+  const Shape& rs = a->value.shape;
+  if (rs.size() < 2 || rs[0] < 2) return ls;
+  for (int qi = 0; qi < 2; ++qi) {
+    const Var& q = a->inputs[qi];
+    const Shape& qs = q.value().shape;
+    if (!q.requires_grad() || qs.size() != rs.size() || qs[0] != 1) continue;
+    if (!std::equal(qs.begin() + 1, qs.end(), rs.begin() + 1)) continue;
+    if (a->inputs[1 - qi].value().shape != rs) continue;
+    ls.add = a;
+    ls.qi = qi;
+    ls.lead = rs[0];
+    return ls;
+  }
+  return ls;
+}
+
+// The add node's gradients as its VJP and unbroadcast would give them: the
+// norm's dx for the full operand, the leading-dim sum for the broadcast one.
+std::vector<std::optional<Tensor>> add_grads(const LeadSum& ls, const std::optional<Tensor>& dx, const Tensor& dsum) {
+  std::vector<std::optional<Tensor>> g(2);
+  const Var& p = ls.add->inputs[1 - ls.qi];
+  if (p.requires_grad()) g[1 - ls.qi] = dx;
+  g[ls.qi] = t_reshape(dsum, ls.add->inputs[ls.qi].value().shape);
+  return g;
+}
+}  // namespace
+
 // graph.rs:373-438
 //
-// One addition to the reference's loop: when an activation node (gelu, silu)
-// takes a norm node's output and that output feeds no other edge of this
-// graph, the activation's VJP and the norm's run as one pass
-// (oxi_*_norm_act_bwd). The norm output's gradient is still formed and
-// stored, and the norm's input gradients are held until the loop reaches the
-// norm node, so every accumulation happens in the reference's order with the
-// same values.
+// Additions to the reference's loop, each giving the same gradients with
+// fewer passes over HBM (OXI_FUSE_NORM_ACT=0 turns them off):
+// - when an activation node (gelu, silu, softmax, log_softmax) takes a norm
+//   node's output, or, for the elementwise ones, a permuted view of it, and
+//   that output feeds no other edge of this graph, the activation's VJP and
+//   the norm's run as one pass (oxi_*_norm_act_bwd). The norm output's
+//   gradient is still formed and stored (through the permute node, as its
+//   VJP would pass it), and the norm's input gradients are held until the
+//   loop reaches the norm node, so every accumulation happens in the
+//   reference's order with the same values;
+// - when the norm's input is r = p + q with q broadcast over the leading dim
+//   (a positional table) and r feeds nothing else, the norm pass also forms
+//   q's gradient (oxi_*_norm_bwd_lead_sum), held for the add node.
 void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
   if (!root.requires_grad())
     err_invalid("element 0 of tensors does not require grad and does not have a grad_fn");
@@ -182,11 +239,12 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
       n.node->grad.reset();
     }
   // edges into each node from the nodes of this graph
+  const bool fuse = fuse_norm_act();
   std::unordered_map<const Node*, int> uses;
-  if (fuse_norm_act())
+  if (fuse)
     for (const Var& n : order)
       for (const Var& in : n.node->inputs) ++uses[in.node.get()];
-  std::unordered_map<const Node*, std::vector<std::optional<Tensor>>> held;  // norm grads from a fused pass
+  std::unordered_map<const Node*, std::vector<std::optional<Tensor>>> held;  // gradients from a fused pass
   root.accumulate_grad(s);
   for (auto it = order.rbegin(); it != order.rend(); ++it) {
     Var& n = *it;
@@ -202,30 +260,52 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
     std::vector<std::optional<Tensor>> grads;
     auto h = held.find(n.node.get());
     if (h != held.end()) {
-      take_vjp(*n.node, retain_graph);  // computed by the fused pass
+      take_vjp(*n.node, retain_graph);  // computed by a fused pass
       grads = std::move(h->second);
       held.erase(h);
     } else {
       Vjp f = take_vjp(*n.node, retain_graph);
       bool done = false;
-      if (n.node->act >= 0 && n.node->inputs.size() == 1 && needs[0]) {
+      if (fuse && n.node->act >= 0 && n.node->inputs.size() == 1 && needs[0]) {
+        // the norm node, directly or through one permute (elementwise activations only)
         Node* nn = n.node->inputs[0].node.get();
-        bool norm_vjp = false;
-        if (nn->norm && uses[nn] == 1) {
-          std::lock_guard<std::mutex> lk(nn->mu);
-          norm_vjp = (bool)nn->vjp;
+        Node* view = nullptr;
+        if (!nn->norm && !nn->perm.empty() && n.node->act <= OXI_ACT_SILU && nn->inputs.size() == 1 &&
+            uses[nn] == 1 && has_vjp(nn)) {
+          view = nn;
+          nn = nn->inputs[0].node.get();
         }
-        if (norm_vjp) {
+        if (nn->norm && uses[nn] == 1 && has_vjp(nn)) {
           std::vector<bool> nneeds;
           for (const Var& in : nn->inputs) nneeds.push_back(in.requires_grad());
-          Tensor dy;
+          Tensor g = *up;
+          if (view) {  // the activation's gradient in the norm output's layout
+            std::vector<int64_t> inv(view->perm.size());
+            for (size_t i = 0; i < inv.size(); ++i) inv[(size_t)view->perm[i]] = (int64_t)i;
+            g = t_permute(g, inv);
+          }
+          LeadSum ls = lead_sum_of(nn, uses);
+          Tensor dy, dsum;
           std::vector<std::optional<Tensor>> ng;
-          if (aops::norm_act_vjp(*nn->norm, n.node->act, *up, nneeds, dy, ng)) {
-            grads = {dy};
+          bool ok = ls.add && aops::norm_vjp_fused(*nn->norm, n.node->act, g, nneeds, &dy, ng, ls.lead, &dsum);
+          if (ok) held[ls.add] = add_grads(ls, ng[0], dsum);
+          else ok = aops::norm_vjp_fused(*nn->norm, n.node->act, g, nneeds, &dy, ng);
+          if (ok) {
+            grads = {view ? t_permute(dy, view->perm) : dy};
             held[nn] = std::move(ng);
             done = true;
             g_fused_passes.fetch_add(1);
           }
+        }
+      } else if (fuse && n.node->norm) {
+        // a norm node whose VJP no activation pass took: fold the leading-dim
+        // sum of a broadcast operand of its input into it
+        LeadSum ls = lead_sum_of(n.node.get(), uses);
+        Tensor dsum;
+        if (ls.add && aops::norm_vjp_fused(*n.node->norm, OXI_ACT_NONE, *up, needs, nullptr, grads, ls.lead, &dsum)) {
+          held[ls.add] = add_grads(ls, grads[0], dsum);
+          done = true;
+          g_fused_passes.fetch_add(1);
         }
       }
       if (!done) grads = f(*up, needs);

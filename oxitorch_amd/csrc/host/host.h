@@ -188,6 +188,7 @@ struct Node {
   bool requires_grad = false;
   std::shared_ptr<const NormSaved> norm;  // set on layer_norm / rms_norm nodes
   int act = -1;                            // OXI_ACT_* on gelu / silu nodes
+  std::vector<int64_t> perm;               // on permute / transpose nodes: the forward order
 };
 
 class Var {
@@ -247,8 +248,14 @@ NormVjp norm_vjp_mode();  // OXI_NORM_VJP=ref|exact (default ref)
 // gradient): fills dy (the norm output's gradient) and one gradient per norm
 // input as `need` asks. False, with nothing computed, when the rows do not
 // vectorize; the caller then runs the two VJPs.
-bool norm_act_vjp(const NormSaved& s, int act, const Tensor& g, const std::vector<bool>& need, Tensor& dy,
-                  std::vector<std::optional<Tensor>>& grads);
+// The norm's VJP as one pass with what backward folds into it: an activation
+// on the norm output (act >= 0: g is the activation's upstream gradient and
+// *dy receives the norm output's gradient; OXI_ACT_NONE: g is the norm
+// output's gradient) and, with lsum, the sum of dx over a leading dim of
+// `lead` rows (*lsum receives it, shape (rows / lead, H)). Returns false,
+// having run nothing, when the kernels do not take this shape.
+bool norm_vjp_fused(const NormSaved& s, int act, const Tensor& g, const std::vector<bool>& need, Tensor* dy,
+                    std::vector<std::optional<Tensor>>& grads, int64_t lead = 0, Tensor* lsum = nullptr);
 Var rms_norm(const Var& x, const Var& w, float eps, NormVjp mode);
 Var layer_norm(const Var& x, const std::optional<Var>& w, const std::optional<Var>& b, float eps, NormVjp mode);
 Var gelu(const Var& x, int approximate);

@@ -90,10 +90,42 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
+// Float reductions over a full wave64 through DPP lane permutes, which run in
+// the VALU pipeline (a __shfl_xor is an LDS-crossbar round trip, and a
+// butterfly chains six of them). Within each row of 16 lanes: swap with the
+// neighbour (xor 1), then within quads (xor 2), then mirror within halves of
+// 8 and within the row; each step combines a lane with a partner lane that
+// holds the mirrored partial, so with a commutative op (+, fmaxf) every lane
+// ends with the same bits. The four row results are then combined in fixed
+// order through readlane, so the result is uniform and deterministic. All
+// 64 lanes must be active, as for the butterfly.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float readlane_f32(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;  // quad_perm:[1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;  // quad_perm:[2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+template <>
+__device__ __forceinline__ float wave_sum<float>(float v) {
+  v += dpp_f32<DPP_QUAD_XOR1>(v);
+  v += dpp_f32<DPP_QUAD_XOR2>(v);
+  v += dpp_f32<DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_f32<DPP_ROW_MIRROR>(v);
+  return (readlane_f32(v, 0) + readlane_f32(v, 16)) + (readlane_f32(v, 32) + readlane_f32(v, 48));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, dpp_f32<DPP_QUAD_XOR1>(v));
+  v = fmaxf(v, dpp_f32<DPP_QUAD_XOR2>(v));
+  v = fmaxf(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
+  v = fmaxf(v, dpp_f32<DPP_ROW_MIRROR>(v));
+  return fmaxf(fmaxf(readlane_f32(v, 0), readlane_f32(v, 16)), fmaxf(readlane_f32(v, 32), readlane_f32(v, 48)));
 }
 
 // Sum across the `TPR` threads of a row group. TPR is 64 (one wave, no LDS)

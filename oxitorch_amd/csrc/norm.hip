@@ -141,15 +141,21 @@ __global__ __launch_bounds__(BS) void norm_fwd_loop_k(const float* __restrict__ 
 // Threads per backward block: one-wave rows run 16 to a block (one block per
 // CU: 16 waves in flight, one partial row per CU), or 8 to a block (two
 // blocks per CU) when 4 float4s per lane would not fit the registers of 16;
-// wider rows 1 per block.
-template <int TPR, int NV>
-constexpr int bwd_threads() { return TPR == 64 ? (NV <= 3 ? 1024 : 512) : TPR; }
+// wider rows 1 per block. The leading-sum walk (LSUM) runs 4 waves to a
+// block, each with LSUM_DEPTH rows in flight.
+template <int TPR, int NV, bool LSUM = false>
+constexpr int bwd_threads() { return LSUM ? 256 : TPR == 64 ? (NV <= 3 ? 1024 : 512) : TPR; }
+constexpr int LSUM_THREADS = 256;
+#ifndef OXI_LSUM_DEPTH
+#define OXI_LSUM_DEPTH 4
+#endif
+constexpr int LSUM_DEPTH = OXI_LSUM_DEPTH;
 
 // ACT_NONE: g is the norm output's gradient. Otherwise g is the gradient of
 // act(y) and the kernel first forms dy (written to dyo if set): g * act'(y)
 // for the elementwise activations, the softmax VJP over the row for
 // OXI_ACT_SOFTMAX / OXI_ACT_LOG_SOFTMAX.
-constexpr int ACT_NONE = -1;
+constexpr int ACT_NONE = OXI_ACT_NONE;
 constexpr bool is_softmax_act(int act) { return act == OXI_ACT_SOFTMAX || act == OXI_ACT_LOG_SOFTMAX; }
 
 template <int ACT>
@@ -159,14 +165,16 @@ __device__ __forceinline__ float act_vjp(float y, float g) {
   else return SiluBwd{}(y, g);
 }
 
-template <int TPR, int NV, int MODE, bool LN, bool NTS, int ACT>
-__global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
+template <int TPR, int NV, int MODE, bool LN, bool NTS, int ACT, bool LSUM>
+__global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM>())) void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  const float* __restrict__ b,
                                                  const float* __restrict__ mean, const float* __restrict__ rstd,
                                                  const float* __restrict__ g, float* __restrict__ dyo,
                                                  float* __restrict__ dx,
-                                                 float* __restrict__ part, int64_t rows, int H) {
-  constexpr int NT = bwd_threads<TPR, NV>();
+                                                 float* __restrict__ part, int64_t rows, int H,
+                                                 float* __restrict__ lsum, int64_t T) {
+  static_assert(!LSUM || TPR == 64, "the leading-sum walk takes one-wave rows");
+  constexpr int NT = bwd_threads<TPR, NV, LSUM>();
   constexpr int GPB = NT / TPR;
   constexpr int ROWF = TPR * NV * 4;  // floats a group covers
   __shared__ float lds[2 * (NT / 64)];
@@ -183,32 +191,48 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
 #pragma unroll
   for (int k = 0; k < NV; ++k) { pdw[k] = zero; pdb[k] = zero; }
 
-  // Wide rows (TPR > 64) keep the loop-invariant weights (and, for the
-  // activation prologue, biases) in registers: a load inside the row loop is
-  // younger than the next row's prefetch, and the in-order vmcnt wait for it
-  // also waits for the prefetch. One-wave rows run 16 waves to a CU at up to
-  // 128 VGPRs, where those registers cost more than the wait: they re-read
-  // w and b (cached) per row. Padding lanes (c >= h4) are zeroed at use.
+  // The loop-invariant weights (and, for the activation prologue, biases)
+  // never load inside the row loop: such a load is younger than the next
+  // row's prefetch, and the in-order vmcnt wait for it would also wait for
+  // the prefetch. Wide rows (TPR > 64) keep them in registers; one-wave rows
+  // run 16 waves to a CU at up to 128 VGPRs and read them from LDS, staged
+  // once per block. Padding lanes (c >= h4) are zeroed at use.
   constexpr bool REG_W = TPR > 64;
+  constexpr int WL = REG_W ? 1 : TPR * NV;  // float4s of w (and b) in LDS
+  __shared__ f4 wl[WL], bl[WL];
   f4 wr[NV], br[NV];
+  const bool need_b = ACT != ACT_NONE && LN && b;
+  if constexpr (REG_W) {
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int cc = min(k * TPR + t, h4 - 1);
-    wr[k] = (REG_W && w) ? w4[cc] : f4{1.f, 1.f, 1.f, 1.f};
-    br[k] = (REG_W && ACT != ACT_NONE && LN && b) ? b4[cc] : zero;
+    for (int k = 0; k < NV; ++k) {
+      const int cc = min(k * TPR + t, h4 - 1);
+      wr[k] = w ? w4[cc] : f4{1.f, 1.f, 1.f, 1.f};
+      br[k] = need_b ? b4[cc] : zero;
+    }
+  } else {
+    for (int c = threadIdx.x; c < WL; c += NT) {
+      const int cc = min(c, h4 - 1);
+      wl[c] = w ? w4[cc] : f4{1.f, 1.f, 1.f, 1.f};
+      bl[c] = need_b ? b4[cc] : zero;
+    }
+    __syncthreads();
   }
-  auto wv_at = [&](int k) -> f4 {
-    const int c = k * TPR + t;
-    if constexpr (REG_W) return c < h4 ? wr[k] : zero;
-    else return c < h4 ? (w ? w4[c] : f4{1.f, 1.f, 1.f, 1.f}) : zero;
+  auto w_at = [&](int k) -> f4 {  // w's float4 k of this lane (in range lanes)
+    if constexpr (REG_W) return wr[k];
+    else return wl[k * TPR + t];
   };
+  auto b_at = [&](int k) -> f4 {
+    if constexpr (REG_W) return br[k];
+    else return bl[k * TPR + t];
+  };
+  auto wv_at = [&](int k) -> f4 { return k * TPR + t < h4 ? w_at(k) : zero; };
 
   // Rows are double-buffered: the next row's x, g and statistics are in
-  // flight while the current row is reduced and stored. For wide rows the
-  // two register sets swap roles every row (the loop is unrolled twice, so
-  // no copies) and every prefetch load issues (row and column clamped in
-  // bounds), so the wait before a row's first use counts exactly the
-  // younger loads.
+  // flight while the current row is reduced and stored. The two register
+  // sets swap roles every row (the loop is unrolled twice, so no copies: a
+  // copy of a loading register waits for its load) and every prefetch load
+  // issues (row and column clamped in bounds), so the wait before a row's
+  // first use counts exactly the younger loads.
   const int64_t ngroups = (int64_t)gridDim.x * GPB;
   int64_t row = (int64_t)blockIdx.x * GPB + gi;
   int red = 0;  // reductions so far: consecutive ones use alternate LDS slot sets
@@ -234,8 +258,8 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
         const int c = k * TPR + t;
         if (c < h4) {
           f4 yv = LN ? (xt.v[k] - mu) * inv : xt.v[k] * inv;
-          if (w) yv = yv * (REG_W ? wr[k] : w4[c]);
-          if (LN && b) yv = yv + (REG_W ? br[k] : b4[c]);
+          if (w) yv = yv * w_at(k);
+          if (LN && b) yv = yv + b_at(k);
           pk[k] = yv;
           m = fmaxf(m, max4(yv));
         } else {
@@ -279,8 +303,8 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
         if (k * TPR + t < h4) {
           const int c = k * TPR + t;
           f4 yv = LN ? (xt.v[k] - mu) * inv : xt.v[k] * inv;
-          if (w) yv = yv * (REG_W ? wr[k] : w4[c]);
-          if (LN && b) yv = yv + (REG_W ? br[k] : b4[c]);
+          if (w) yv = yv * w_at(k);
+          if (LN && b) yv = yv + b_at(k);
           const f4 gv = gt.v[k];
           gt.v[k] = f4{act_vjp<ACT>(yv.x, gv.x), act_vjp<ACT>(yv.y, gv.y), act_vjp<ACT>(yv.z, gv.z),
                        act_vjp<ACT>(yv.w, gv.w)};
@@ -338,35 +362,74 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV>())) void norm_bwd_k(const flo
   };
   RowTile<TPR, NV> xa, ga, xb, gb;
   float ia = 0.f, ma = 0.f, ib = 0.f, mb = 0.f;
-  if constexpr (!REG_W) {
-    RowTile<TPR, NV> xt, gt;
-    float inv = 0.f, mu = 0.f;
-    if (row < rows) {
-      xt.load(x + row * H, h4, t);
-      gt.load(g + row * H, h4, t);
-      inv = rstd[row];
-      if constexpr (LN) mu = mean[row];
-    }
-    while (row < rows) {
-      const int64_t nrow = row + ngroups;
-      RowTile<TPR, NV> xn, gn;
-      float ninv = 0.f, nmu = 0.f;
-      if (nrow < rows) {
-        xn.load(x + nrow * H, h4, t);
-        gn.load(g + nrow * H, h4, t);
-        ninv = rstd[nrow];
-        if constexpr (LN) nmu = mean[nrow];
+  // The scheduling barriers keep the current row's first use below the next
+  // row's loads, so its wait leaves those loads in flight.
+  if constexpr (LSUM) {
+    // Rows are (lead, T): row b * T + p is batch b at position p. Each wave
+    // owns positions p = wave, wave + waves, ... and walks a position's rows
+    // in batch order, LSUM_DEPTH rows in flight (the row sequence continues
+    // into the wave's next position), adding each dx row to a register sum
+    // that starts from 0.0f: the sequential sum oxi_reduce(SUM) forms over
+    // the leading dim, bit for bit. No barriers. lead is a multiple of
+    // LSUM_DEPTH (the host checks), so every round processes LSUM_DEPTH rows
+    // and every refill load issues: the waits count exactly the younger
+    // loads. The last round's refills re-read the wave's last row (cache).
+    const int lead = (int)(rows / T);
+    const int waves = (int)gridDim.x * GPB;
+    const int wave = (int)blockIdx.x * GPB + gi;
+    const int npos = wave < T ? (int)((T - 1 - wave) / waves + 1) : 0;
+    const int nj = npos * lead;  // this wave's rows
+    const int last_p = wave + (npos - 1) * waves;
+    int fb = 0, fp = wave;  // the next row to fetch: batch fb at position fp
+    int cb = 0, cp = wave;  // the next row to process
+    auto fetch_next = [&](RowTile<TPR, NV>& xt, RowTile<TPR, NV>& gt, float& inv, float& mu) {
+      const int64_t r = fp <= last_p ? (int64_t)fb * T + fp : (int64_t)(lead - 1) * T + last_p;
+      fetch(xt, gt, inv, mu, r);
+      if (++fb == lead) {
+        fb = 0;
+        fp += waves;
       }
-      process(xt, gt, inv, mu, row);
-      xt = xn;
-      gt = gn;
-      inv = ninv;
-      mu = nmu;
-      row = nrow;
+    };
+    if (nj > 0) {
+      RowTile<TPR, NV> xs[LSUM_DEPTH], gs[LSUM_DEPTH];
+      float is[LSUM_DEPTH], ms[LSUM_DEPTH];
+      f4 acc[NV];
+#pragma unroll
+      for (int d = 0; d < LSUM_DEPTH; ++d) fetch_next(xs[d], gs[d], is[d], ms[d]);
+      for (int j0 = 0; j0 < nj; j0 += LSUM_DEPTH) {
+#pragma unroll
+        for (int d = 0; d < LSUM_DEPTH; ++d) {
+          process(xs[d], gs[d], is[d], ms[d], (int64_t)cb * T + cp);  // gs[d] now holds the row's dx
+          if (cb == 0) {
+#pragma unroll
+            for (int q = 0; q < NV; ++q) acc[q] = zero;
+          }
+#pragma unroll
+          for (int q = 0; q < NV; ++q) acc[q] = acc[q] + gs[d].v[q];
+          if (cb == lead - 1) {
+            f4* o = reinterpret_cast<f4*>(lsum + (int64_t)cp * H);
+#pragma unroll
+            for (int q = 0; q < NV; ++q)
+              if (q * TPR + t < h4) st_stream<NTS>(acc[q], o + q * TPR + t);
+          }
+          if (++cb == lead) {
+            cb = 0;
+            cp += waves;
+          }
+          // the refill reuses the slot's registers after their last use
+          __builtin_amdgcn_sched_barrier(0);
+          fetch_next(xs[d], gs[d], is[d], ms[d]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  } else if ((int64_t)rows <= ngroups) {
+    // at most one row per group (e.g. 4096 rows of 768): nothing to prefetch
+    if (row < rows) {
+      fetch(xa, ga, ia, ma, row);
+      process(xa, ga, ia, ma, row);
     }
   } else {
-    // The scheduling barriers keep the current row's first use below the next
-    // row's loads, so its wait leaves those loads in flight.
     fetch(xa, ga, ia, ma, row);
     while (row < rows) {
       fetch(xb, gb, ib, mb, row + ngroups);
@@ -564,12 +627,28 @@ int launch_fwd(const float* x, const float* w, const float* b, float* y, float* 
 template <bool LN, int MODE, bool NTS, int ACT>
 void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x, const float* w, const float* b,
                     const float* mean, const float* rstd, const float* g, float* dyo, float* dx, float* part,
-                    int64_t rows, int h) {
+                    int64_t rows, int h, float* lsum, int64_t T) {
 #define OXI_BWD(TPR, NV)                                                                                   \
   case TPR * 10 + NV:                                                                                      \
-    norm_bwd_k<TPR, NV, MODE, LN, NTS, ACT><<<dim3((unsigned)nblk), dim3(nt), 0, s>>>(                     \
-        x, w, b, mean, rstd, g, dyo, dx, part, rows, h);                                                   \
+    norm_bwd_k<TPR, NV, MODE, LN, NTS, ACT, false><<<dim3((unsigned)nblk), dim3(nt), 0, s>>>(              \
+        x, w, b, mean, rstd, g, dyo, dx, part, rows, h, nullptr, 0);                                       \
     break;
+#define OXI_BWD_LSUM(NV)                                                                                   \
+  case 640 + NV:                                                                                           \
+    norm_bwd_k<64, NV, MODE, LN, NTS, ACT, true><<<dim3((unsigned)nblk), dim3(LSUM_THREADS), 0, s>>>(      \
+        x, w, b, mean, rstd, g, dyo, dx, part, rows, h, lsum, T);                                          \
+    break;
+  if (lsum) {  // one-wave rows only (lsum_check)
+    switch (cfg) {
+      OXI_BWD_LSUM(1)
+      OXI_BWD_LSUM(2)
+      OXI_BWD_LSUM(3)
+      OXI_BWD_LSUM(4)
+      default:
+        break;
+    }
+    return;
+  }
   switch (cfg) {
     OXI_BWD(64, 1)
     OXI_BWD(64, 2)
@@ -584,6 +663,7 @@ void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x
         norm_bwd_loop_k<MODE, LN><<<dim3((unsigned)nblk), dim3(BS), 0, s>>>(x, w, mean, rstd, g, dx, part, rows, h);
   }
 #undef OXI_BWD
+#undef OXI_BWD_LSUM
 }
 
 // Bytes of column partials the backward needs for (rows, H): 2 x blocks x H
@@ -602,20 +682,23 @@ size_t bwd_part_bytes(bool need_part, int64_t rows, int64_t H, int cfg) {
 // `fixed` (when not null) holds at least bwd_part_bytes() bytes of device
 // memory for the column partials; otherwise they come from the caching
 // allocator.
+// lsum (with lead > 0): also write lsum (rows / lead, H) = the sum of dx over
+// the leading dim of a (lead, rows / lead) row grid; the caller has checked
+// lsum_ok().
 template <bool LN, int MODE, int ACT = ACT_NONE>
 int launch_bwd(const float* x, const float* w, const float* b, const float* mean, const float* rstd,
                const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H,
-               void* fixed = nullptr) {
+               void* fixed = nullptr, float* lsum = nullptr, int64_t lead = 0) {
   hipStream_t s = stream();
   const bool need_part = dw || (LN && db);
   const int cfg = vec_ok(H, {x, w, b, g, dyo, dx}) ? pick_bwd_cfg(H / 4) : 0;
   if (ACT != ACT_NONE && cfg == 0) return fail(OXI_OTHER, "norm_act_bwd: internal: unvectorized fused launch");
   const int tpr = cfg ? cfg / 10 : BS;
-  const int nt = tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : tpr;  // bwd_threads<TPR, NV>()
+  const int nt = lsum ? LSUM_THREADS : tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : tpr;  // bwd_threads<>()
   const int gpb = nt / tpr;
   // Blocks: enough to fill the chip, few enough that the partial rows stay
   // a small fraction of the row traffic.
-  int64_t nblk = ceil_div(rows, gpb);
+  int64_t nblk = lsum ? ceil_div(rows / lead, gpb) : ceil_div(rows, gpb);  // lsum: a wave per position
   // (measured: 2 blocks per CU beat 3 and 4 for 4096-float rows)
   const int64_t cap = (int64_t)cu_count() * (nt == 1024 ? 1 : 2);
   if (need_part && nblk > cap) nblk = cap;
@@ -627,10 +710,11 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   // may have more blocks than bwd_part_bytes() sizes for)
   float* part = !need_part ? nullptr : fixed ? static_cast<float*>(fixed) : ws.as<float>();
   const int h = (int)H;
+  const int64_t T = lsum ? rows / lead : 0;
   if (nt_stores(rows * H * 4))
-    launch_bwd_cfg<LN, MODE, true, ACT>(cfg, s, nblk, nt, x, w, b, mean, rstd, g, dyo, dx, part, rows, h);
+    launch_bwd_cfg<LN, MODE, true, ACT>(cfg, s, nblk, nt, x, w, b, mean, rstd, g, dyo, dx, part, rows, h, lsum, T);
   else
-    launch_bwd_cfg<LN, MODE, false, ACT>(cfg, s, nblk, nt, x, w, b, mean, rstd, g, dyo, dx, part, rows, h);
+    launch_bwd_cfg<LN, MODE, false, ACT>(cfg, s, nblk, nt, x, w, b, mean, rstd, g, dyo, dx, part, rows, h, lsum, T);
   int rc = check_launch(LN ? "layer_norm_bwd" : "rms_norm_bwd");
   if (rc != OXI_OK) return rc;
   if (need_part) {
@@ -643,25 +727,49 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
 
 template <bool LN, int MODE>
 int launch_act_bwd(int act, const float* x, const float* w, const float* b, const float* mean, const float* rstd,
-                   const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H) {
+                   const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H,
+                   float* lsum = nullptr, int64_t lead = 0) {
   switch (act) {
+    case OXI_ACT_NONE:
+      return launch_bwd<LN, MODE>(x, w, b, mean, rstd, g, nullptr, dx, dw, db, rows, H, nullptr, lsum, lead);
     case OXI_ACT_GELU_TANH:
-      return launch_bwd<LN, MODE, OXI_ACT_GELU_TANH>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+      return launch_bwd<LN, MODE, OXI_ACT_GELU_TANH>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H, nullptr,
+                                                     lsum, lead);
     case OXI_ACT_GELU_ERF:
-      return launch_bwd<LN, MODE, OXI_ACT_GELU_ERF>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+      return launch_bwd<LN, MODE, OXI_ACT_GELU_ERF>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H, nullptr, lsum,
+                                                    lead);
     case OXI_ACT_SILU:
-      return launch_bwd<LN, MODE, OXI_ACT_SILU>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+      return launch_bwd<LN, MODE, OXI_ACT_SILU>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H, nullptr, lsum,
+                                                lead);
     case OXI_ACT_SOFTMAX:
-      return launch_bwd<LN, MODE, OXI_ACT_SOFTMAX>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+      return launch_bwd<LN, MODE, OXI_ACT_SOFTMAX>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H, nullptr, lsum,
+                                                   lead);
     default:
-      return launch_bwd<LN, MODE, OXI_ACT_LOG_SOFTMAX>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H);
+      return launch_bwd<LN, MODE, OXI_ACT_LOG_SOFTMAX>(x, w, b, mean, rstd, g, dyo, dx, dw, db, rows, H, nullptr,
+                                                       lsum, lead);
   }
+}
+
+// Whether the leading-dim sum fits the launch: one-wave rows (a wave walks
+// a position's rows), rows a multiple of lead.
+int lsum_check(const char* what, int64_t lead, int64_t rows, int64_t cols, const float* dx, const float* dx_sum) {
+  if (lead < 1 || rows % lead != 0)
+    return fail(OXI_INVALID_ARGUMENT, "%s: %lld rows are not a multiple of lead %lld", what, (long long)rows,
+                (long long)lead);
+  if (lead % LSUM_DEPTH != 0 || rows / lead > ((int64_t)1 << 30))
+    return fail(OXI_NOT_IMPLEMENTED, "%s: lead %lld is not a multiple of %d (or positions exceed 2^30); run the VJP "
+                "and the reduction", what, (long long)lead, LSUM_DEPTH);
+  if (!dx || !dx_sum) return fail(OXI_INVALID_ARGUMENT, "%s: dx and dx_sum must not be NULL", what);
+  if (pick_bwd_cfg(cols / 4) / 10 != 64)
+    return fail(OXI_NOT_IMPLEMENTED, "%s: rows of %lld floats are wider than one wave; run the VJP and the reduction",
+                what, (long long)cols);
+  return OXI_OK;
 }
 
 // Shared checks of the fused entry points; OXI_OK means "launch".
 int check_act(const char* what, int act, int mode, const float* x, const float* w, const float* b, const float* g,
-              const float* dyo, const float* dx, int64_t rows, int64_t cols) {
-  if (act < OXI_ACT_GELU_TANH || act > OXI_ACT_LOG_SOFTMAX)
+              const float* dyo, const float* dx, int64_t rows, int64_t cols, bool allow_none = false) {
+  if ((act < OXI_ACT_GELU_TANH || act > OXI_ACT_LOG_SOFTMAX) && !(allow_none && act == OXI_ACT_NONE))
     return fail(OXI_INVALID_ARGUMENT, "%s: unknown activation %d", what, act);
   if (mode != OXI_NORM_VJP_REF && mode != OXI_NORM_VJP_EXACT)
     return fail(OXI_INVALID_ARGUMENT, "%s: unknown VJP mode %d", what, mode);
@@ -773,6 +881,39 @@ int oxi_layer_norm_bwd_noalloc(const float* x, const float* w, const float* mean
              ? launch_bwd<true, OXI_NORM_VJP_REF>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols, sp)
              : launch_bwd<true, OXI_NORM_VJP_EXACT>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols,
                                                     sp);
+}
+
+int oxi_rms_norm_bwd_lead_sum(const float* x, const float* w, const float* rstd, const float* g, int act, float* dy,
+                              float* dx, float* dw, float* dx_sum, int64_t lead, int64_t rows, int64_t cols,
+                              int mode) {
+  if (int rc = check_rows("rms_norm_bwd_lead_sum", x, g, rows, cols)) return rc;
+  if (!rstd && rows) return fail(OXI_INVALID_ARGUMENT, "rms_norm_bwd_lead_sum: rstd must not be NULL");
+  if (int rc = check_act("rms_norm_bwd_lead_sum", act, mode, x, w, nullptr, g, dy, dx, rows, cols, true)) return rc;
+  if (rows == 0 || cols == 0) return fail(OXI_NOT_IMPLEMENTED, "rms_norm_bwd_lead_sum: empty rows; run the VJP");
+  if (int rc = lsum_check("rms_norm_bwd_lead_sum", lead, rows, cols, dx, dx_sum)) return rc;
+  OXI_CHECK_INIT();
+  return mode == OXI_NORM_VJP_REF
+             ? launch_act_bwd<false, OXI_NORM_VJP_REF>(act, x, w, nullptr, nullptr, rstd, g, dy, dx, dw, nullptr,
+                                                       rows, cols, dx_sum, lead)
+             : launch_act_bwd<false, OXI_NORM_VJP_EXACT>(act, x, w, nullptr, nullptr, rstd, g, dy, dx, dw, nullptr,
+                                                         rows, cols, dx_sum, lead);
+}
+
+int oxi_layer_norm_bwd_lead_sum(const float* x, const float* w, const float* b, const float* mean, const float* rstd,
+                                const float* g, int act, float* dy, float* dx, float* dw, float* db, float* dx_sum,
+                                int64_t lead, int64_t rows, int64_t cols, int mode) {
+  if (int rc = check_rows("layer_norm_bwd_lead_sum", x, g, rows, cols)) return rc;
+  if ((!rstd || !mean) && rows)
+    return fail(OXI_INVALID_ARGUMENT, "layer_norm_bwd_lead_sum: mean/rstd must not be NULL");
+  if (int rc = check_act("layer_norm_bwd_lead_sum", act, mode, x, w, b, g, dy, dx, rows, cols, true)) return rc;
+  if (rows == 0 || cols == 0) return fail(OXI_NOT_IMPLEMENTED, "layer_norm_bwd_lead_sum: empty rows; run the VJP");
+  if (int rc = lsum_check("layer_norm_bwd_lead_sum", lead, rows, cols, dx, dx_sum)) return rc;
+  OXI_CHECK_INIT();
+  return mode == OXI_NORM_VJP_REF
+             ? launch_act_bwd<true, OXI_NORM_VJP_REF>(act, x, w, b, mean, rstd, g, dy, dx, dw, db, rows, cols, dx_sum,
+                                                      lead)
+             : launch_act_bwd<true, OXI_NORM_VJP_EXACT>(act, x, w, b, mean, rstd, g, dy, dx, dw, db, rows, cols,
+                                                        dx_sum, lead);
 }
 
 int oxi_rms_norm_act_bwd(const float* x, const float* w, const float* rstd, const float* g, int act, float* dy,

@@ -14,7 +14,7 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import assert_close, rng
+from conftest import assert_close, assert_sum_close, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -329,3 +329,105 @@ def test_graph_fusion_x_grad_only_and_exact_mode(ox, vjp):
             _native.set_fuse_norm_act(prev)
     assert _native.fused_norm_act_passes() - before == 1
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+# ---- the leading-dim sum folded into the norm VJP ------------------------------------------
+
+LEAD_SHAPES = [(16, 1024, 768), (4, 300, 256), (8, 64, 1024), (4, 7, 36), (12, 5, 768), (16, 3, 64), (32, 40, 512)]
+
+
+@pytest.mark.parametrize("act", ["none", "silu", "gelu_erf", "softmax"])
+@pytest.mark.parametrize("norm", ["rms_norm", "layer_norm"])
+@pytest.mark.parametrize("lts", LEAD_SHAPES)
+def test_lead_sum_matches_vjp_and_reduce(hip, lts, norm, act):
+    """dy, dx and the leading-dim sum are the bits of the separate VJP(s) and
+    oxi_reduce(SUM) over dim 0; dw / db are the same column sums added in
+    another row order, so they agree to the sum's conditioning."""
+    lead, T, H = lts
+    say("lead-sum VJP", norm, lts, act)
+    x, w, b, g = _inputs((lead * T, H), 31)
+    dx_, dw_, db_, dg = D(hip, x), D(hip, w), D(hip, b), D(hip, g)
+    if norm == "layer_norm":
+        y, mean, rstd = hip.layer_norm_fwd(dx_, dw_, db_, 1e-5)
+    else:
+        y, rstd = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+    dyv = dg if act == "none" else _act_bwd(hip, y, dg, act)
+    if norm == "layer_norm":
+        dx2, dw2, db2 = hip.layer_norm_bwd(dx_, dw_, mean, rstd, dyv)
+        dy, dx, dw, db, ds = hip.layer_norm_bwd_lead_sum(dx_, dw_, db_, mean, rstd, dg, lead, act=act)
+    else:
+        dx2, dw2 = hip.rms_norm_bwd(dx_, dw_, rstd, dyv)
+        dy, dx, dw, ds = hip.rms_norm_bwd_lead_sum(dx_, dw_, rstd, dg, lead, act=act)
+    if act != "none":
+        _same(dy, dyv, "dy")
+    _same(dx, dx2, "dx")
+    ds2 = hip.reduce("sum", dx2, 0, shape=(lead, T, H), x_strides=(T * H, H, 1))
+    assert np.array_equal(ds.numpy().reshape(T, H).view(np.uint32), ds2.numpy().reshape(T, H).view(np.uint32)), \
+        "dx_sum differs from oxi_reduce over the leading dim"
+    # column sums in another order: |difference| within rtol * sum|terms|
+    yv, dyn = y.numpy().astype(np.float64), dyv.numpy().astype(np.float64)
+    xh = (yv - b if norm == "layer_norm" else yv) / w  # the normalised input, up to rounding
+    assert_sum_close(dw.numpy(), dw2.numpy(), np.abs(dyn * xh).sum(0), what="dw")
+    if norm == "layer_norm":
+        assert_sum_close(db.numpy(), db2.numpy(), np.abs(dyn).sum(0), what="db")
+
+
+def test_lead_sum_refusals(hip):
+    say("lead-sum VJP refusals")
+    for (rows, H, lead, exc) in [(3 * 4, 768, 3, NotImplementedError), (1 * 5, 768, 1, NotImplementedError),
+                                 (16 * 4, 2048, 16, NotImplementedError), (30, 768, 16, ValueError)]:
+        x, w, _, g = _inputs((rows, H), 32)
+        dx_, dw_ = D(hip, x), D(hip, w)
+        _, rstd = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+        with pytest.raises(exc):
+            hip.rms_norm_bwd_lead_sum(dx_, dw_, rstd, D(hip, g), lead)
+
+
+# ---- the graph rules on config 5's chain ------------------------------------------------------
+
+def _c5_chain(ox, F, fuse, B, T, H, V, seed):
+    from oxitorch_amd import _native
+    r = rng(seed)
+    Wa = r.standard_normal((V, H), dtype=np.float32)
+    ids = r.integers(0, V, B * T)
+    lnw, lnb, rw = (r.standard_normal(H, dtype=np.float32) for _ in range(3))
+    pos = r.standard_normal((1, T, H), dtype=np.float32)
+    g = r.standard_normal((B, T, H), dtype=np.float32)
+    prev = _native.set_fuse_norm_act(fuse)
+    try:
+        n0 = _native.fused_norm_act_passes()
+        W, LW, LB, RW, P = (ox.from_numpy(a, True) for a in (Wa, lnw, lnb, rw, pos))
+        h = F.layer_norm(F.embedding(ids, W).reshape([B, T, H]), LW, LB)
+        s = F.silu(h.permute([0, 2, 1]))
+        n = F.rms_norm(s.permute([0, 2, 1]) + P, RW)
+        y = F.softmax(n, -1)
+        y.backward(ox.from_numpy(g))
+        passes = _native.fused_norm_act_passes() - n0
+        out = {"y": y.numpy(), "W": W.grad.numpy(), "lnw": LW.grad.numpy(), "lnb": LB.grad.numpy(),
+               "rw": RW.grad.numpy(), "pos": P.grad.numpy(), "dn": n.grad.numpy(), "n": n.numpy(),
+               "rw_value": rw}
+        return out, passes
+    finally:
+        _native.set_fuse_norm_act(prev)
+
+
+@pytest.mark.parametrize("dims", [(16, 128, 768), (4, 33, 256), (16, 1024, 768)])
+def test_c5_graph_fusions(ox, dims):
+    """Config 5's backward with the graph fusions (layer_norm + silu through the
+    permute, rms_norm + softmax with the positional gradient) against the
+    reference's node-by-node order: the same bits except rms_norm's weight
+    gradient, a column sum taken in another row order."""
+    from oxitorch_amd.nn import functional as F
+    B, T, H = dims
+    say("C5 graph fusions", dims)
+    fused, passes = _c5_chain(ox, F, True, B, T, H, 5000, 41)
+    plain, none = _c5_chain(ox, F, False, B, T, H, 5000, 41)
+    assert passes == 2 and none == 0, (passes, none)
+    for k in ("y", "W", "lnw", "lnb", "pos", "dn"):
+        a, b = fused[k], plain[k]
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{dims}: {k} differs"
+    # drw = sum over rows of dn * xhat (xhat = n / rw): both sums hold the same
+    # terms in another order, so they differ by at most rtol * sum |terms|
+    xh = fused["n"].astype(np.float64).reshape(-1, H) / fused["rw_value"]
+    terms = np.abs(fused["dn"].astype(np.float64).reshape(-1, H) * xh).sum(0)
+    assert_sum_close(fused["rw"], plain["rw"], terms, what="drw")
