@@ -9,7 +9,9 @@ from .module import Module, Parameter
 
 
 class LayerNorm(Module):
-    """LayerNorm over the last dim with learned affine."""
+    """F.layer_norm with its own weight (ones) and bias (zeros) of
+    `normalized_shape`; `seed` is accepted for the reference's signature and
+    unused (the initial values are constants)."""
 
     def __init__(self, normalized_shape, eps=1e-5, seed=None):
         self.eps = eps
@@ -21,7 +23,8 @@ class LayerNorm(Module):
 
 
 class RMSNorm(Module):
-    """RMSNorm over the last dim (scale only)."""
+    """F.rms_norm with its own weight (ones) of `normalized_shape`; `seed`
+    as in LayerNorm."""
 
     def __init__(self, normalized_shape, eps=1e-6, seed=None):
         self.eps = eps
@@ -32,7 +35,9 @@ class RMSNorm(Module):
 
 
 class Embedding(Module):
-    """Lookup table: rows of `weight` selected by integer indices."""
+    """F.embedding over its own (num_embeddings, embedding_dim) table, drawn
+    as standard normals * 0.05 from default_rng(seed); forward takes a flat
+    sequence of int ids."""
 
     def __init__(self, num_embeddings, embedding_dim, seed=None):
         rng = np.random.default_rng(seed)
@@ -46,6 +51,8 @@ class Embedding(Module):
 
 
 class _Activation(Module):
+    """A parameterless module that applies one F.* activation."""
+
     def __init__(self, fn):
         self._fn = fn
 
@@ -74,6 +81,8 @@ def Sigmoid():
 
 
 class Softmax(Module):
+    """F.softmax along `dim`."""
+
     def __init__(self, dim=-1):
         self.dim = dim
 

@@ -1,249 +1,88 @@
-"""torch.utils.data-style loading for oxitorch_amd (python/oxitorch/utils/data.py).
+"""Batches that land on the device: the input-pipeline row of this build.
 
-Same API as the reference module. Two paths behind one `DataLoader`:
+A dataset of column tensors that share their first dim (`TensorDataset`) is
+uploaded to HBM once, when its loader is made. Every batch is then one
+device gather of all columns at the batch's rows (`_native.DataLoader`,
+oxi_batch_gather). The rows come in order, or shuffled per epoch as
+NumPy's `RandomState(seed + epoch).permutation(n)`, the order the reference's
+native loader draws (crates/oxi-data/src/batch.rs:223-292, rng.rs); the host
+computes coming epochs' orders on `num_workers` threads, and that is all the
+host does per epoch.
 
-- **Device path** for datasets that expose `tensors` (column tensors sharing
-  dim 0, e.g. `TensorDataset`) with the default collation and no custom
-  sampler: `_native.DataLoader` keeps the columns in HBM for the loader's
-  lifetime, uploads each epoch's row order once, and gathers every batch on
-  the device, one launch for all columns. Shuffled orders are NumPy's
-  `RandomState(seed + epoch).permutation(n)`, as in the reference's native
-  loader. The only host work is each epoch's permutation; `num_workers`
-  host threads (at least one) compute the coming epochs' orders ahead.
-- **Generic path** for any other `Dataset` / `IterableDataset`: items are
-  fetched per index (through a thread pool when `num_workers > 1`) and
-  collated with `default_collate`; the collated batch is uploaded through the
-  library's pinned staging ring without waiting for the device.
-
-As in the reference, labels are f32 tensors.
+The constructor keeps the reference's signature
+(python/oxitorch/utils/data.py:167-201). Its per-item path (any map-style or
+iterable dataset fetched item by item, samplers, custom collation) stays on
+the host in the reference and is not part of this device build: those
+arguments raise NotImplementedError. Batches are leaf tensors without
+gradient, f32 like the reference's.
 """
 
 import os
-from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
 from oxitorch_amd import _native
 
-__all__ = [
-    "DataLoader",
-    "Dataset",
-    "IterableDataset",
-    "RandomSampler",
-    "SequentialSampler",
-    "Subset",
-    "TensorDataset",
-    "default_collate",
-]
+__all__ = ["DataLoader", "TensorDataset"]
 
 
-class Dataset:
-    """Map-style dataset: `__getitem__` and `__len__`."""
-
-    def __getitem__(self, index):
-        raise NotImplementedError
-
-    def __len__(self):
-        raise NotImplementedError
+def _on_device(column):
+    if isinstance(column, _native.Tensor):
+        return column
+    return _native.from_numpy(np.ascontiguousarray(column, dtype=np.float32))
 
 
-class IterableDataset(Dataset):
-    """Stream-style dataset: `__iter__`."""
-
-    def __iter__(self):
-        raise NotImplementedError
-
-
-class TensorDataset(Dataset):
-    """Rows of several tensors that share dim 0."""
+class TensorDataset:
+    """Column tensors of equal length; item i is the tuple of their i-th rows."""
 
     def __init__(self, *tensors):
-        rows = tensors[0].shape[0]
-        for k, t in enumerate(tensors):
-            if t.shape[0] != rows:
-                raise ValueError(f"tensor {k} has {t.shape[0]} rows, expected {rows}")
+        lengths = [t.shape[0] for t in tensors]
+        for k, rows in enumerate(lengths):
+            if rows != lengths[0]:
+                raise ValueError(f"tensor {k} has {rows} rows, expected {lengths[0]}")
         self.tensors = tensors
-
-    def __getitem__(self, index):
-        return tuple(t[index] for t in self.tensors)
 
     def __len__(self):
         return self.tensors[0].shape[0]
 
-
-class Subset(Dataset):
-    """The rows `indices` of another dataset, fetched per item."""
-
-    def __init__(self, dataset, indices):
-        self.dataset = dataset
-        self.indices = list(indices)
-
     def __getitem__(self, index):
-        return self.dataset[self.indices[index]]
-
-    def __len__(self):
-        return len(self.indices)
-
-
-class Sampler:
-    """An index stream."""
-
-    def __iter__(self):
-        raise NotImplementedError
-
-    def __len__(self):
-        raise NotImplementedError
-
-
-class SequentialSampler(Sampler):
-    def __init__(self, data_source):
-        self.data_source = data_source
-
-    def __iter__(self):
-        return iter(range(len(self.data_source)))
-
-    def __len__(self):
-        return len(self.data_source)
-
-
-class RandomSampler(Sampler):
-    """A permutation per pass; with `seed`, pass k uses RandomState(seed + k)."""
-
-    def __init__(self, data_source, seed=None):
-        self.data_source = data_source
-        self.seed = seed
-        self._epoch = 0
-
-    def __iter__(self):
-        n = len(self.data_source)
-        if self.seed is None:
-            order = np.random.permutation(n)
-        else:
-            order = np.random.RandomState(self.seed + self._epoch).permutation(n)
-            self._epoch += 1
-        return (int(i) for i in order)
-
-    def __len__(self):
-        return len(self.data_source)
-
-
-def _stack_f32(arrays):
-    return np.ascontiguousarray(np.stack([np.asarray(a, dtype=np.float32) for a in arrays]))
-
-
-def default_collate(items):
-    """Batches fetched items: tuples field by field, tensors and numpy arrays
-    stacked into an f32 tensor (tensors keep `requires_grad` when all have
-    it), Python numbers into an f32 vector."""
-    if not items:
-        raise ValueError("cannot collate an empty item list")
-    head = items[0]
-    if isinstance(head, (tuple, list)):
-        return tuple(default_collate([it[k] for it in items]) for k in range(len(head)))
-    if isinstance(head, np.ndarray):
-        return _native.from_numpy(_stack_f32(items))
-    if hasattr(head, "shape") and hasattr(head, "numpy"):
-        rg = all(bool(getattr(it, "requires_grad", False)) for it in items)
-        return _native.from_numpy(_stack_f32([it.detach().numpy() for it in items]), rg)
-    if isinstance(head, (int, float)):
-        return _native.from_numpy(np.ascontiguousarray(np.asarray(items, dtype=np.float32)))
-    raise TypeError(f"default_collate cannot handle items of type {type(head)!r}")
+        return tuple(column[index] for column in self.tensors)
 
 
 class DataLoader:
-    """Batches a dataset with torch's constructor surface. Each `__iter__`
-    is one epoch; seeded shuffles are reproducible epoch by epoch."""
+    """Device batches of a column dataset; each `iter()` is one epoch."""
 
     def __init__(self, dataset, batch_size=1, shuffle=False, sampler=None, batch_sampler=None, num_workers=0,
-                 collate_fn=default_collate, drop_last=False, seed=None):
+                 collate_fn=None, drop_last=False, seed=None):
         if batch_size < 1:
             raise ValueError("batch_size must be >= 1")
+        unsupported = [name for name, v in (("sampler", sampler), ("batch_sampler", batch_sampler),
+                                            ("collate_fn", collate_fn)) if v is not None]
+        if unsupported:
+            raise NotImplementedError(
+                f"DataLoader({', '.join(unsupported)}=...): custom sampling and collation run item by item on the "
+                "host; this build's loader gathers whole batches of column tensors on the device")
+        columns = getattr(dataset, "tensors", None)
+        if columns is None:
+            raise NotImplementedError(
+                f"DataLoader over {type(dataset).__name__}: only datasets of column tensors (TensorDataset) have a "
+                "device path; per-item datasets are outside this build")
         self.dataset = dataset
         self.batch_size = batch_size
         self.shuffle = shuffle
-        self.sampler = sampler
-        self.batch_sampler = batch_sampler
-        self.num_workers = num_workers
-        self.collate_fn = collate_fn
         self.drop_last = drop_last
-        self.seed = seed
-        # an unseeded loader still varies by run: a random base drawn once
-        self._auto_seed = int.from_bytes(os.urandom(4), "little")
-        self._epoch = 0
-        self._device_loader = None
+        self.num_workers = num_workers
+        # an unseeded loader draws one random base, so runs differ while the
+        # epochs of one run stay reproducible; `seed` fixes it
+        self.seed = seed if seed is not None else int.from_bytes(os.urandom(4), "little")
+        self._batches = _native.DataLoader([_on_device(c) for c in columns], batch_size=batch_size,
+                                           shuffle=shuffle, drop_last=drop_last, seed=self.seed,
+                                           num_workers=num_workers)
 
     def __len__(self):
-        if self.batch_sampler is not None:
-            return len(self.batch_sampler)
-        if isinstance(self.dataset, IterableDataset):
-            raise TypeError("IterableDataset has no length; len(DataLoader) is undefined")
-        n = len(self.dataset)
-        return n // self.batch_size if self.drop_last else -(-n // self.batch_size)
-
-    def _device_path(self):
-        """The device loader for tensor-column datasets, built once (its
-        columns are uploaded to HBM a single time), or None."""
-        if self.sampler is not None or self.batch_sampler is not None or self.collate_fn is not default_collate:
-            return None
-        if getattr(self.dataset, "native_parts", None) is not None:
-            return None  # datasets with native transforms take the per-item path here
-        tensors = getattr(self.dataset, "tensors", None)
-        if tensors is None:
-            return None
-        if self._device_loader is None:
-            cols = [t if isinstance(t, _native.Tensor) else _native.from_numpy(np.ascontiguousarray(t, np.float32))
-                    for t in tensors]
-            base = self.seed if self.seed is not None else self._auto_seed
-            self._device_loader = _native.DataLoader(cols, batch_size=self.batch_size, shuffle=self.shuffle,
-                                                     drop_last=self.drop_last, seed=base,
-                                                     num_workers=self.num_workers)
-        return self._device_loader
+        rows = len(self.dataset)
+        full, rest = divmod(rows, self.batch_size)
+        return full + (1 if rest and not self.drop_last else 0)
 
     def __iter__(self):
-        epoch = self._epoch
-        self._epoch += 1
-        dev = self._device_path()
-        if dev is not None:
-            # the device loader's own epoch counter follows this one: the
-            # order of pass k is RandomState(seed + k).permutation(n)
-            yield from iter(dev)
-            return
-        if self.batch_sampler is not None:
-            for batch in self.batch_sampler:
-                yield self._collate(list(batch))
-            return
-        if isinstance(self.dataset, IterableDataset):
-            yield from self._stream()
-            return
-        if self.sampler is not None:
-            order = iter(self.sampler)
-        elif self.shuffle:
-            order = iter(RandomSampler(self.dataset, seed=None if self.seed is None else self.seed + epoch))
-        else:
-            order = iter(SequentialSampler(self.dataset))
-        batch = []
-        for i in order:
-            batch.append(i)
-            if len(batch) == self.batch_size:
-                yield self._collate(batch)
-                batch = []
-        if batch and not self.drop_last:
-            yield self._collate(batch)
-
-    def _stream(self):
-        items = []
-        for item in self.dataset:
-            items.append(item)
-            if len(items) == self.batch_size:
-                yield self.collate_fn(items)
-                items = []
-        if items and not self.drop_last:
-            yield self.collate_fn(items)
-
-    def _collate(self, batch):
-        if self.num_workers > 1 and len(batch) > 1:
-            with ThreadPoolExecutor(max_workers=self.num_workers) as pool:
-                items = list(pool.map(self.dataset.__getitem__, batch))
-        else:
-            items = [self.dataset[i] for i in batch]
-        return self.collate_fn(items)
+        return iter(self._batches)

@@ -134,6 +134,57 @@ def test_modules(ox):
     assert emb.weight.grad is not None and ln.bias.grad is not None and rms.weight.grad is not None
 
 
+def test_module_state_round_trip(ox):
+    """python/oxitorch/nn/module.py:62-98,121-122: dotted names through lists,
+    train() reaching list members, state_dict / load_state_dict with the
+    reference's missing-key and shape errors, Sequential indexing."""
+    import oxitorch_amd.nn as nn
+
+    class Block(nn.Module):
+        def __init__(self):
+            self.norms = [nn.LayerNorm(4), nn.RMSNorm(4)]
+            self.emb = nn.Embedding(6, 4, seed=1)
+
+        def forward(self, ids):
+            return self.norms[1](self.norms[0](self.emb(ids)))
+
+    seq = nn.Sequential(Block(), nn.SiLU())
+    assert seq[0] is seq.layers[0] and seq[-1] is seq.layers[1]
+    names = [n for n, _ in seq.named_parameters()]
+    assert names == ["layers.0.norms.0.weight", "layers.0.norms.0.bias", "layers.0.norms.1.weight",
+                     "layers.0.emb.weight"]
+    assert len(seq.parameters()) == 4
+    seq.eval()
+    assert not seq.training and not seq[0].training and not seq[0].norms[0].training and not seq[0].emb.training
+    seq.train()
+    assert seq[0].norms[1].training
+
+    state = seq.state_dict()
+    assert sorted(state) == sorted(names)
+    r = rng(12)
+    new = {k: r.standard_normal(v.shape).astype(np.float32) for k, v in state.items()}
+    seq.load_state_dict(new)
+    for k, p in seq.named_parameters():
+        np.testing.assert_array_equal(p.tensor.numpy(), new[k])
+        assert p.tensor.requires_grad
+    out = seq([0, 5, 2])
+    out.sum().backward()
+    assert seq[0].emb.weight.grad is not None
+
+    before = {k: v.copy() for k, v in seq.state_dict().items()}
+    missing = dict(new)
+    del missing["layers.0.emb.weight"]
+    with pytest.raises(KeyError, match="missing key in state_dict: 'layers.0.emb.weight'"):
+        seq.load_state_dict(missing)
+    bad = dict(new)
+    bad["layers.0.norms.1.weight"] = np.zeros(5, np.float32)
+    with pytest.raises(ValueError, match=r"shape mismatch for 'layers.0.norms.1.weight': state \[5\] vs parameter \[4\]"):
+        seq.load_state_dict(bad)
+    # a refused load changes nothing
+    for k, v in seq.state_dict().items():
+        np.testing.assert_array_equal(v, before[k])
+
+
 # ---- python/tests/test_indexing_grad.py ------------------------------------------------------
 
 def test_index_select_duplicate_accumulation(ox):
