@@ -702,7 +702,7 @@ int build_plan(const int64_t* idx, int64_t n, int64_t len, hipStream_t s, SortPl
   if (passes == 0) passes = 1;
   const size_t ints = 4 * (size_t)n + 256 * (size_t)rtiles + (size_t)len + 1;
   p->ws = ws_alloc(ints * sizeof(int));
-  if (!p->ws) return OXI_OTHER;
+  if (!p->ws) return fail_alloc("index_select_bwd: sort workspace");
   int* keys = static_cast<int*>(p->ws);
   int* pos = keys + n;
   int* keys2 = pos + n;
@@ -752,7 +752,7 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   // end tile per key and the owner list of long keys; partial rows
   Workspace wsi(((size_t)len + (size_t)stiles) * sizeof(int));
   Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(float));
-  if (!wsi.p || !wsp.p) return OXI_OTHER;
+  if (!wsi.p || !wsp.p) return fail_alloc("index_select_bwd: apply workspace");
   int* end_tile = wsi.as<int>();
   int* owners = end_tile + len;
   const int* ka = p.ka;

@@ -594,7 +594,7 @@ int oxi_scatter_rows(const float* base, int64_t rows, int64_t inner, const int64
     return fail(OXI_INVALID_ARGUMENT, "scatter_rows: NULL pointer");
   OXI_CHECK_INIT();
   Workspace ws(sizeof(int) * (size_t)rows);
-  if (!ws.p) return fail(OXI_OTHER, "scatter_rows: workspace allocation failed");
+  if (!ws.p) return fail_alloc("scatter_rows: workspace");
   int* w = ws.as<int>();
   winners(idx, n, rows, w);
   const bool vec = inner % 4 == 0 && al16(base) && al16(out) && (n == 0 || al16(values));
@@ -624,7 +624,7 @@ int oxi_scatter_rows_bwd(const float* g, int64_t rows, int64_t inner, const int6
   if (!gbase && !gvalues) return OXI_OK;
   OXI_CHECK_INIT();
   Workspace ws(sizeof(int) * (size_t)rows);
-  if (!ws.p) return fail(OXI_OTHER, "scatter_rows_bwd: workspace allocation failed");
+  if (!ws.p) return fail_alloc("scatter_rows_bwd: workspace");
   int* w = ws.as<int>();
   winners(idx, n, rows, w);
   const bool vec = inner % 4 == 0 && al16(g) && (!gbase || al16(gbase)) && (!gvalues || al16(gvalues));
@@ -680,7 +680,7 @@ int oxi_masked_select(const float* x, const int64_t* x_strides, const float* mas
   const bool fast1 = contiguous(g1, 0) && al16(x);
   Workspace wc(sizeof(int) * (size_t)T);
   Workspace wr(record ? 0 : (size_t)record_bytes(T));
-  if (!wc.p || (!record && !wr.p)) return fail(OXI_OTHER, "masked_select: workspace allocation failed");
+  if (!wc.p || (!record && !wr.p)) return fail_alloc("masked_select: workspace");
   int64_t* offs = static_cast<int64_t*>(record ? record : wr.p);
   uint64_t* rec = reinterpret_cast<uint64_t*>(offs + T + 1);
   hipStream_t st = stream();
@@ -699,7 +699,7 @@ int oxi_masked_select(const float* x, const int64_t* x_strides, const float* mas
   }
   if (total == 0) return OXI_OK;
   void* buf = nullptr;
-  if ((rc = oxi_hip_alloc(sizeof(float) * (size_t)total, &buf)) != OXI_OK) return rc;
+  if (oxi_hip_alloc(sizeof(float) * (size_t)total, &buf) != OXI_OK) return fail_alloc("masked_select: output");
   float* o = static_cast<float*>(buf);
   if (fast1) msel_write_k<true><<<(unsigned)T, MB, 0, st>>>(g1, x, E, offs, rec, o);
   else msel_write_k<false><<<(unsigned)T, MB, 0, st>>>(g1, x, E, offs, rec, o);
@@ -744,7 +744,7 @@ int oxi_masked_select_bwd(const void* record, const int64_t* shape, int ndim, co
   const int64_t* offs = static_cast<const int64_t*>(record);
   const uint64_t* rec = reinterpret_cast<const uint64_t*>(offs + T + 1);
   Workspace wt(bcast ? sizeof(float) * (size_t)E : 0);
-  if (bcast && !wt.p) return fail(OXI_OTHER, "masked_select_bwd: workspace allocation failed");
+  if (bcast && !wt.p) return fail_alloc("masked_select_bwd: workspace");
   // the gradient layout: x's own (no broadcast) or a dense grid-order buffer
   int64_t rms[MAXD];
   int64_t acc = 1;

@@ -16,6 +16,9 @@ namespace oxi {
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Maps a failing HIP call to OXI_OTHER with its name and HIP error string.
 int fail_hip(hipError_t err, const char* what);
+// After a failed oxi_hip_alloc / ws_alloc: OXI_OTHER with `what` (the call
+// site) in front of the allocator's own message.
+int fail_alloc(const char* what);
 // Stream of the initialised device; initialises device 0 on first use.
 // Returns nullptr and sets the error when no device can be initialised.
 bool ensure_init();

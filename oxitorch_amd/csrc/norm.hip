@@ -705,7 +705,7 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
   if (nblk < 1) nblk = 1;
   Workspace ws(need_part && !fixed ? sizeof(float) * 2 * (size_t)nblk * (size_t)H : 0);
-  if (need_part && !fixed && !ws.p) return OXI_OTHER;
+  if (need_part && !fixed && !ws.p) return fail_alloc("norm VJP: column partials");
   // no partials without dw/db: the kernel then writes none (its launch shape
   // may have more blocks than bwd_part_bytes() sizes for)
   float* part = !need_part ? nullptr : fixed ? static_cast<float*>(fixed) : ws.as<float>();

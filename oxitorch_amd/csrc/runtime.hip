@@ -120,6 +120,11 @@ int fail_hip(hipError_t err, const char* what) {
   return fail(OXI_OTHER, "%s failed: %s", what, hipGetErrorString(err));
 }
 
+int fail_alloc(const char* what) {
+  const std::string cause = g_last_error;
+  return fail(OXI_OTHER, "%s: %s", what, cause.c_str());
+}
+
 bool initialised() {
   Runtime& r = rt();
   std::lock_guard<std::mutex> lk(r.mu);

@@ -452,7 +452,7 @@ int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets, float* lo
   if (c == 0) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: zero classes");
   if (!logits || !targets || !lse) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: NULL tensor pointer");
   Workspace picked(sizeof(float) * (size_t)n);
-  if (!picked.p) return OXI_OTHER;
+  if (!picked.p) return fail_alloc("cross_entropy_fwd: workspace");
   const int vec = (c % 4 == 0 && aligned16({logits})) ? 1 : 0;
   ce_fwd_k<<<dim3((unsigned)n), dim3(CE_BS), 0, stream()>>>(logits, targets, lse, picked.as<float>(), n, (int)c, vec,
                                                             guard_flag());
