@@ -907,6 +907,14 @@ def time_dropin(hip, wl, steps, warmup):
     for _ in range(max(warmup, 1)):
         step()
     hip.sync()
+    # enough steps for about 0.2 s, so that the host settles into its
+    # steady state (a few steps time the first ones only)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        step()
+    hip.sync()
+    est = (time.perf_counter() - t0) / 3
+    steps = max(steps, min(2000, int(0.2 / max(est, 1e-6))))
     t = hip.Timer()
     t.start()
     h0 = time.perf_counter()
@@ -915,8 +923,8 @@ def time_dropin(hip, wl, steps, warmup):
     h1 = time.perf_counter()
     ms = t.stop() / steps
     hip.sync()
-    return {"what": wl.dropin_what, "ms_per_step": round(ms, 5), "host_ms_per_step": round((h1 - h0) * 1e3 / steps, 5),
-            "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 2)}
+    return {"what": wl.dropin_what, "steps": steps, "ms_per_step": round(ms, 5),
+            "host_ms_per_step": round((h1 - h0) * 1e3 / steps, 5), "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 2)}
 
 
 def run_config(hip, key, args):

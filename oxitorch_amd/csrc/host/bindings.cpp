@@ -140,6 +140,59 @@ PyTensor select_impl(const PyTensor& self, int64_t dim, int64_t index) {
   return leaf(t_select(t, dim, index));
 }
 
+// Integer ids as PyO3 extracts a Vec<i64>: any sequence of integers (items
+// with __index__; floats and str are refused with TypeError, values outside
+// int64 with OverflowError). A 1-d numpy integer array is read through its
+// buffer instead of item by item: that is the embedding's hot input.
+std::vector<int64_t> int_ids(const py::handle& obj) {
+  if (py::isinstance<py::array>(obj)) {
+    const py::array a = py::reinterpret_borrow<py::array>(obj);
+    const char kind = a.dtype().kind();
+    if (a.ndim() == 1 && (kind == 'i' || kind == 'u')) {
+      const auto c = py::array_t<int64_t, py::array::c_style | py::array::forcecast>::ensure(a);
+      if (!c) throw py::error_already_set();
+      if (kind == 'u' && a.dtype().itemsize() == 8) {
+        // uint64 values above INT64_MAX do not fit, as for a Python int
+        const auto u = py::array_t<uint64_t, py::array::c_style | py::array::forcecast>::ensure(a);
+        for (py::ssize_t i = 0; i < u.size(); ++i)
+          if (u.data()[i] > (uint64_t)INT64_MAX) {
+            PyErr_SetString(PyExc_OverflowError, "Python int too large to convert to C long long");
+            throw py::error_already_set();
+          }
+      }
+      return std::vector<int64_t>(c.data(), c.data() + c.size());
+    }
+  }
+  if (PyUnicode_Check(obj.ptr())) throw py::type_error("Can't extract `str` to `Vec`");
+  PyObject* seq = PySequence_Fast(obj.ptr(), "expected a sequence of integers");
+  if (!seq) throw py::error_already_set();
+  const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
+  PyObject** items = PySequence_Fast_ITEMS(seq);
+  std::vector<int64_t> out((size_t)n);
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* it = items[i];
+    long long v;
+    if (PyLong_CheckExact(it)) {
+      v = PyLong_AsLongLong(it);
+    } else {
+      PyObject* ix = PyNumber_Index(it);
+      if (!ix) {
+        Py_DECREF(seq);
+        throw py::error_already_set();
+      }
+      v = PyLong_AsLongLong(ix);
+      Py_DECREF(ix);
+    }
+    if (v == -1 && PyErr_Occurred()) {
+      Py_DECREF(seq);
+      throw py::error_already_set();
+    }
+    out[(size_t)i] = (int64_t)v;
+  }
+  Py_DECREF(seq);
+  return out;
+}
+
 PyTensor index_select_impl(const PyTensor& self, int64_t dim, const std::vector<int64_t>& idx) {
   if (self.v.requires_grad()) return PyTensor(aops::index_select(self.v, dim, idx));
   return leaf(t_index_select(self.value(), dim, idx));
@@ -418,11 +471,13 @@ PYBIND11_MODULE(_native, m) {
            })
       .def("narrow", &narrow_impl)
       .def("select", &select_impl)
-      .def("index_select", &index_select_impl)
-      .def("gather", [](const PyTensor& s, const std::vector<int64_t>& idx) { return index_select_impl(s, 0, idx); })
+      .def("index_select",
+           [](const PyTensor& s, int64_t dim, const py::object& idx) { return index_select_impl(s, dim, int_ids(idx)); })
+      .def("gather", [](const PyTensor& s, const py::object& idx) { return index_select_impl(s, 0, int_ids(idx)); })
       // bindings lib.rs:650-673: differentiable when either operand needs a gradient
       .def("scatter",
-           [](const PyTensor& s, const std::vector<int64_t>& idx, const PyTensor& values) {
+           [](const PyTensor& s, const py::object& ids, const PyTensor& values) {
+             const std::vector<int64_t> idx = int_ids(ids);
              if (s.v.requires_grad() || values.v.requires_grad())
                return PyTensor(aops::scatter_dim0(s.v, idx, values.v));
              return leaf(t_scatter_dim0(s.value(), idx, values.value()));
@@ -530,11 +585,11 @@ PYBIND11_MODULE(_native, m) {
   m.def(
       "log_softmax", [](const PyTensor& x, int64_t dim) { return PyTensor(aops::softmax(x.v, dim, true)); },
       py::arg("x"), py::arg("dim") = -1);
-  m.def("cross_entropy", [](const PyTensor& logits, const std::vector<int64_t>& targets) {
-    return PyTensor(aops::cross_entropy(logits.v, targets));
+  m.def("cross_entropy", [](const PyTensor& logits, const py::object& targets) {
+    return PyTensor(aops::cross_entropy(logits.v, int_ids(targets)));
   });
-  m.def("embedding", [](const std::vector<int64_t>& indices, const PyTensor& w) {
-    return PyTensor(aops::embedding(indices, w.v));
+  m.def("embedding", [](const py::object& indices, const PyTensor& w) {
+    return PyTensor(aops::embedding(int_ids(indices), w.v));
   });
 
   // Elementwise clamp on the device (binary max then min against scalar

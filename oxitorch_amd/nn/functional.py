@@ -101,9 +101,11 @@ def rms_norm(x, weight, eps=1e-6, vjp=None):
 # ---- embedding (functional.py:245-247) -----------------------------------------------
 
 def embedding(indices, weight):
-    """`weight` is `(num_embeddings, dim)`; `indices` is a flat sequence of ints."""
-    idx = np.asarray(indices, dtype=np.int64).ravel().tolist()
-    return _native.embedding(idx, weight)
+    """`weight` is `(num_embeddings, dim)`; `indices` is a flat sequence of
+    ints, or a numpy integer array of any shape (read in C order)."""
+    if isinstance(indices, np.ndarray):
+        indices = indices.ravel()
+    return _native.embedding(indices, weight)
 
 
 # ---- losses (functional.py:270-293) -----------------------------------------------------
@@ -129,7 +131,7 @@ def cross_entropy(logits, targets):
     if bad.any():
         raise IndexError(f"index {int(t[bad][0])} is out of bounds for axis 1 with size {classes}")
     t = np.where(t < 0, t + classes, t)
-    return _native.cross_entropy(logits, t.tolist())
+    return _native.cross_entropy(logits, t)
 
 
 def linear(*args, **kwargs):

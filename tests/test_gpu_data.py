@@ -60,6 +60,29 @@ def test_many_small_uploads_wrap_the_ring(hip):
     assert np.array_equal(dev.numpy().reshape(n, sz), want)
 
 
+@pytest.mark.parametrize("offset", [0, 1, 4, 8, 12, 15])
+def test_small_uploads_any_alignment(hip, offset):
+    """Uploads up to 1 MiB are copied by a kernel: destinations at every
+    offset mod 16, sizes around the 16-byte vector width and the 1 MiB limit,
+    interleaved with DMA uploads, and the bytes either side left alone."""
+    say("small uploads at offset", offset)
+    sizes = [1, 3, 15, 16, 17, 255, 4096 + 5, (1 << 20) - 1, 1 << 20, (1 << 20) + 1, 3 << 20]
+    total = sum(sizes) + 64 * len(sizes) + 64
+    dev = hip.DeviceArray((total,), np.uint8)
+    fill = np.full(total, 0xA5, np.uint8)
+    hip.call("oxi_hip_upload", dev.ptr, fill.ctypes.data, total)
+    want = fill.copy()
+    r = rng(offset)
+    at = offset
+    for sz in sizes:
+        a = r.integers(0, 256, sz, dtype=np.uint8)
+        hip.call("oxi_hip_upload", dev.ptr + at, a.ctypes.data, sz)
+        want[at:at + sz] = a
+        a[:] = 0
+        at += sz + 64
+    assert np.array_equal(dev.numpy(), want)
+
+
 def test_pinned_async_copy(hip):
     say("pinned h2d_async")
     nbytes = 8 << 20
