@@ -234,7 +234,8 @@ class C2(Workload):
 
     # The host core's default for this config: the norm output feeds only the
     # GELU, so backward runs both VJPs as one pass (oxi_layer_norm_act_bwd
-    # reads x and g, writes dy and dx) and a step crosses HBM 8 E-sized times
+    # reads x and g and writes dx; the norm output's gradient is formed only
+    # if its .grad is read) and a step crosses HBM 7 E-sized times
     # (moved_bytes), not the 10 of the per-op count the metric is defined on.
     # unfused_kernels() is the path with that fusion off (OXI_FUSE_NORM_ACT=0)
     # or with other consumers of the norm output.
@@ -246,8 +247,8 @@ class C2(Workload):
         E4 = R * H * 4
         return self.unfused_kernels()[:2] + [
             ("layer_norm_gelu_bwd", lambda: c(L.oxi_layer_norm_act_bwd(
-                self.x.ptr, self.w.ptr, self.b.ptr, self.mean.ptr, self.rstd.ptr, self.g.ptr, 1, self.dh.ptr,
-                self.dx.ptr, self.dw.ptr, self.db.ptr, R, H, 0)), 4 * E4)]
+                self.x.ptr, self.w.ptr, self.b.ptr, self.mean.ptr, self.rstd.ptr, self.g.ptr, 1, None,
+                self.dx.ptr, self.dw.ptr, self.db.ptr, R, H, 0)), 3 * E4)]
 
     def cpu_step(self, ref, lo, hi):
         h = self.host
@@ -376,9 +377,10 @@ class C5(Workload):
                              embedding_bwd=ID + E4 + VH4)
         self.bytes_per_step = 26 * E4 + VH4 + 2 * P4 + 2 * ID
         # the default backward's fused passes: rms_norm + softmax VJP with the
-        # positional gradient (read r, g; write dn, dr, dpos), layer_norm +
-        # silu VJP through the permute (read e, dr; write dh, de)
-        self.op_bytes.update(rms_norm_softmax_pos_bwd=4 * E4 + P4, layer_norm_silu_bwd=4 * E4)
+        # positional gradient (read r, g; write dr, dpos), layer_norm + silu
+        # VJP through the permute (read e, dr; write de). Neither writes the
+        # norm output's gradient: the host core forms it when .grad is read.
+        self.op_bytes.update(rms_norm_softmax_pos_bwd=3 * E4 + P4, layer_norm_silu_bwd=3 * E4)
 
     def unfused_kernels(self):
         L, c = self.hip.lib, self.hip.check
@@ -434,12 +436,12 @@ class C5(Workload):
                 continue
             if name == "rms_norm_bwd":
                 out.append(("rms_norm_softmax_pos_bwd", lambda: c(L.oxi_rms_norm_bwd_lead_sum(
-                    self.r.ptr, self.rw.ptr, self.rs2.ptr, self.g.ptr, 3, self.dn.ptr, self.dr.ptr, self.drw.ptr,
+                    self.r.ptr, self.rw.ptr, self.rs2.ptr, self.g.ptr, 3, None, self.dr.ptr, self.drw.ptr,
                     self.dpos.ptr, self.B, R, H, 0)), b["rms_norm_softmax_pos_bwd"]))
                 continue
             if name == "layer_norm_bwd":
                 out.append(("layer_norm_silu_bwd", lambda: c(L.oxi_layer_norm_act_bwd(
-                    self.e.ptr, self.lnw.ptr, self.lnb.ptr, self.mu.ptr, self.rs1.ptr, self.dr.ptr, 2, self.dh.ptr,
+                    self.e.ptr, self.lnw.ptr, self.lnb.ptr, self.mu.ptr, self.rs1.ptr, self.dr.ptr, 2, None,
                     self.de.ptr, self.dlnw.ptr, self.dlnb.ptr, R, H, 0)), b["layer_norm_silu_bwd"]))
                 continue
             out.append((name, fn, nbytes))

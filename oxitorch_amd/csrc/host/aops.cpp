@@ -474,14 +474,15 @@ bool norm_vjp_fused(const NormSaved& s, int act, const Tensor& g, const std::vec
   grads.assign(need.size(), std::nullopt);
   const bool ndx = need[0] || lsum, ndw = s.wi >= 0 && need[s.wi], ndb = s.bi >= 0 && need[s.bi];
   Tensor gc = t_contiguous(g.shape == s.x.shape ? g : t_broadcast_to(g, s.x.shape));
-  Tensor d = act >= 0 ? Tensor::empty(s.x.shape, Dev::Hip) : Tensor();
+  const bool ndy = act >= 0 && dy;  // the activation's input gradient, when the caller keeps it
+  Tensor d = ndy ? Tensor::empty(s.x.shape, Dev::Hip) : Tensor();
   Tensor dx = ndx ? Tensor::empty(s.x.shape, Dev::Hip) : Tensor();
   Tensor dw = ndw ? Tensor::empty({s.H}, Dev::Hip) : Tensor();
   Tensor db = ndb ? Tensor::empty({s.H}, Dev::Hip) : Tensor();
   Tensor ls = lsum ? Tensor::empty({s.rows / lead, s.H}, Dev::Hip) : Tensor();
   const float* w = s.has_w ? s.w.data() : nullptr;
   const float* b = s.has_b ? s.b.data() : nullptr;
-  float* dp = act >= 0 ? d.data() : nullptr;
+  float* dp = ndy ? d.data() : nullptr;
   float* dxp = ndx ? dx.data() : nullptr;
   float* dwp = ndw ? dw.data() : nullptr;
   float* dbp = ndb ? db.data() : nullptr;
@@ -500,7 +501,7 @@ bool norm_vjp_fused(const NormSaved& s, int act, const Tensor& g, const std::vec
     return false;
   if (rc == OXI_NOT_IMPLEMENTED) return false;
   hip_check(rc);
-  if (dy) *dy = d;
+  if (ndy) *dy = d;
   if (lsum) *lsum = ls;
   if (need[0]) grads[0] = dx;
   if (ndw) grads[s.wi] = dw;

@@ -45,29 +45,50 @@ Var Var::op(Tensor value, const char* name, std::vector<Var> inputs, Vjp vjp) {
   return v;
 }
 
-std::optional<Tensor> Var::grad() const {
-  std::lock_guard<std::mutex> lk(node->mu);
-  return node->grad;
+namespace {
+// The node's gradient, forming a deferred one first (outside the node's lock:
+// forming it launches kernels).
+std::optional<Tensor> read_grad(Node& nd) {
+  std::shared_ptr<DeferredGrad> d;
+  {
+    std::lock_guard<std::mutex> lk(nd.mu);
+    if (nd.grad || !nd.dgrad) return nd.grad;
+    d = nd.dgrad;
+  }
+  Tensor g = d->get();
+  std::lock_guard<std::mutex> lk(nd.mu);
+  if (nd.dgrad == d) {
+    nd.grad = g;
+    nd.dgrad.reset();
+  }
+  return nd.grad;
 }
+}  // namespace
+
+std::optional<Tensor> Var::grad() const { return read_grad(*node); }
 
 void Var::set_grad(const Tensor& g) const {  // graph.rs:208-217
   if (g.shape != node->value.shape) err_shape(fmt_shape(g.shape), fmt_shape(node->value.shape));
   std::lock_guard<std::mutex> lk(node->mu);
   node->grad = g;
+  node->dgrad.reset();
 }
 
 void Var::clear_grad() const {
   std::lock_guard<std::mutex> lk(node->mu);
   node->grad.reset();
+  node->dgrad.reset();
 }
 
 void Var::zero_grad() const {  // graph.rs:229-233
   Tensor z = t_zeros(node->value.shape, node->value.dev());
   std::lock_guard<std::mutex> lk(node->mu);
   node->grad = z;
+  node->dgrad.reset();
 }
 
 void Var::accumulate_grad(const Tensor& g) const {  // graph.rs:235-242
+  (void)read_grad(*node);  // a deferred gradient is formed before anything is added to it
   std::lock_guard<std::mutex> lk(node->mu);
   if (!node->grad) node->grad = g;
   else node->grad = t_add(*node->grad, g);
@@ -216,7 +237,10 @@ std::vector<std::optional<Tensor>> add_grads(const LeadSum& ls, const std::optio
 //   gradient is still formed and stored (through the permute node, as its
 //   VJP would pass it), and the norm's input gradients are held until the
 //   loop reaches the norm node, so every accumulation happens in the
-//   reference's order with the same values;
+//   reference's order with the same values. The pass does not write the
+//   norm output's gradient: that node (and the permute between, if any)
+//   gets it deferred, formed on first read by the activation's own VJP (and
+//   the permute's), so reading it gives the node-by-node values;
 // - when the norm's input is r = p + q with q broadcast over the leading dim
 //   (a positional table) and r feeds nothing else, the norm pass also forms
 //   q's gradient (oxi_*_norm_bwd_lead_sum), held for the add node.
@@ -237,6 +261,7 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
     if (n.node->op) {
       std::lock_guard<std::mutex> lk(n.node->mu);
       n.node->grad.reset();
+      n.node->dgrad.reset();
     }
   // edges into each node from the nodes of this graph
   const bool fuse = fuse_norm_act();
@@ -245,25 +270,36 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
     for (const Var& n : order)
       for (const Var& in : n.node->inputs) ++uses[in.node.get()];
   std::unordered_map<const Node*, std::vector<std::optional<Tensor>>> held;  // gradients from a fused pass
+  std::unordered_set<const Node*> through;  // permutes between a fused activation and its norm
   root.accumulate_grad(s);
   for (auto it = order.rbegin(); it != order.rend(); ++it) {
     Var& n = *it;
     if (!n.node->op) continue;
-    std::optional<Tensor> up;
-    {
-      std::lock_guard<std::mutex> lk(n.node->mu);
-      up = n.node->grad;
-    }
-    if (!up) err_invalid("internal: node reached in backward without a gradient");
-    std::vector<bool> needs;
-    for (const Var& in : n.node->inputs) needs.push_back(in.requires_grad());
     std::vector<std::optional<Tensor>> grads;
     auto h = held.find(n.node.get());
     if (h != held.end()) {
       take_vjp(*n.node, retain_graph);  // computed by a fused pass
       grads = std::move(h->second);
       held.erase(h);
+    } else if (through.count(n.node.get())) {
+      // its gradient is deferred; the norm output's is this permute's VJP of it
+      Vjp fv = take_vjp(*n.node, retain_graph);
+      std::shared_ptr<DeferredGrad> dv;
+      {
+        std::lock_guard<std::mutex> lk(n.node->mu);
+        dv = n.node->dgrad;
+      }
+      auto dn = std::make_shared<DeferredGrad>();
+      dn->make = [fv, dv]() { return *fv(dv->get(), std::vector<bool>{true})[0]; };
+      Node* nn = n.node->inputs[0].node.get();
+      std::lock_guard<std::mutex> lk(nn->mu);
+      nn->dgrad = std::move(dn);
+      continue;
     } else {
+      const std::optional<Tensor> up = read_grad(*n.node);
+      if (!up) err_invalid("internal: node reached in backward without a gradient");
+      std::vector<bool> needs;
+      for (const Var& in : n.node->inputs) needs.push_back(in.requires_grad());
       Vjp f = take_vjp(*n.node, retain_graph);
       bool done = false;
       if (fuse && n.node->act >= 0 && n.node->inputs.size() == 1 && needs[0]) {
@@ -285,13 +321,21 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
             g = t_permute(g, inv);
           }
           LeadSum ls = lead_sum_of(nn, uses);
-          Tensor dy, dsum;
+          Tensor dsum;
           std::vector<std::optional<Tensor>> ng;
-          bool ok = ls.add && aops::norm_vjp_fused(*nn->norm, n.node->act, g, nneeds, &dy, ng, ls.lead, &dsum);
+          bool ok = ls.add && aops::norm_vjp_fused(*nn->norm, n.node->act, g, nneeds, nullptr, ng, ls.lead, &dsum);
           if (ok) held[ls.add] = add_grads(ls, ng[0], dsum);
-          else ok = aops::norm_vjp_fused(*nn->norm, n.node->act, g, nneeds, &dy, ng);
+          else ok = aops::norm_vjp_fused(*nn->norm, n.node->act, g, nneeds, nullptr, ng);
           if (ok) {
-            grads = {view ? t_permute(dy, view->perm) : dy};
+            // the activation's input gradient (its only edge) is formed on read
+            auto d = std::make_shared<DeferredGrad>();
+            d->make = [f, u = *up]() { return *f(u, std::vector<bool>{true})[0]; };
+            Node* ain = n.node->inputs[0].node.get();
+            {
+              std::lock_guard<std::mutex> lk(ain->mu);
+              ain->dgrad = std::move(d);
+            }
+            if (view) through.insert(view);
             held[nn] = std::move(ng);
             done = true;
             g_fused_passes.fetch_add(1);

@@ -178,6 +178,23 @@ struct NormSaved {
   int wi = -1, bi = -1;  // input slots of w and b, -1 when absent
 };
 
+// The gradient of an intermediate that a fused backward pass did not write:
+// formed on first read by the VJP(s) that would have formed it in the
+// node-by-node order, so it holds the same values.
+struct DeferredGrad {
+  std::function<Tensor()> make;
+  std::optional<Tensor> value;
+  std::mutex mu;
+  Tensor get() {
+    std::lock_guard<std::mutex> lk(mu);
+    if (!value) {
+      value = make();
+      make = nullptr;  // drops what the recipe held
+    }
+    return *value;
+  }
+};
+
 struct Node {
   Tensor value;
   const char* op = nullptr;
@@ -185,6 +202,7 @@ struct Node {
   std::mutex mu;
   std::optional<Vjp> vjp;
   std::optional<Tensor> grad;
+  std::shared_ptr<DeferredGrad> dgrad;  // when set (and grad is not), the gradient to form on read
   bool requires_grad = false;
   std::shared_ptr<const NormSaved> norm;  // set on layer_norm / rms_norm nodes
   int act = -1;                            // OXI_ACT_* on gelu / silu nodes

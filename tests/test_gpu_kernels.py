@@ -454,6 +454,27 @@ def test_index_select_bwd_plan_matches_one_call(hip, case):
     hip.sync()
 
 
+@pytest.mark.parametrize("n,V", [(16384, 50257), (16385, 50257), (1, 7), (2, 1), (3000, 65535), (3000, 65536),
+                                 (12000, 16), (9000, 300), (16384, 256), (5000, 257)])
+def test_index_select_bwd_plan_at_sort_limits(hip, n, V):
+    """The plan built on the second stream and the one-call VJP give the same
+    bits around the sort's limits (tile and table sizes, 1 and 2 radix
+    passes, one and two rows), with Zipf ids, repeats and negatives."""
+    say("index_select_bwd plan sort", n, V)
+    r = rng(7 * n + V)
+    ids = np.minimum(r.zipf(1.2, n) - 1, V - 1).astype(np.int64)
+    ids[r.random(n) < 0.1] -= V
+    Dm = 8
+    g = r.standard_normal((n, Dm), dtype=np.float32)
+    dg, di = D(hip, g), D(hip, ids)
+    want = hip.index_select_bwd(dg, (V, Dm), 0, di).numpy()
+    plan = hip.BwdPlan(di, V)
+    got = plan.apply(dg, (V, Dm), 0).numpy()
+    plan.free()
+    hip.sync()
+    np.testing.assert_array_equal(got, want)
+
+
 def _zipf_ids(seed, shape, V):
     r = rng(seed)
     return np.minimum(r.zipf(1.1, shape) - 1, V - 1).astype(np.int64)

@@ -74,6 +74,12 @@ def test_layer_norm_act_bwd_matches_two_vjps(hip, shape, act, mode):
     _same(dx, dx2, "dx")
     _same(dw, dw2, "dw")
     _same(db, db2, "db")
+    # without dy (the graph's default): the same norm gradients
+    none, dx3, dw3, db3 = hip.layer_norm_act_bwd(dx_, dw_, db_, mean, rstd, dg, act, mode=mode, need_dy=False)
+    assert none is None
+    _same(dx3, dx2, "dx without dy")
+    _same(dw3, dw2, "dw without dy")
+    _same(db3, db2, "db without dy")
 
 
 @pytest.mark.parametrize("mode", ["ref", "exact"])
@@ -90,6 +96,10 @@ def test_rms_norm_act_bwd_matches_two_vjps(hip, shape, act, mode):
     _same(dy, dy2, "dy")
     _same(dx, dx2, "dx")
     _same(dw, dw2, "dw")
+    none, dx3, dw3 = hip.rms_norm_act_bwd(dx_, dw_, rstd, dg, act, mode=mode, need_dy=False)
+    assert none is None
+    _same(dx3, dx2, "dx without dy")
+    _same(dw3, dw2, "dw without dy")
 
 
 SOFTMAX_SHAPES = [(512, 768), (64, 1000), (7, 36), (33, 256), (5, 2048), (1, 4), (2, 3, 512)]
@@ -276,6 +286,43 @@ def test_graph_fusion_is_invisible(ox, case, shape):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{case} {shape}: {name}.grad differs"
 
 
+def test_fused_intermediate_grad_is_formed_on_read(ox):
+    """The fused pass leaves the norm output's gradient unwritten; reading
+    .grad forms it (the activation's VJP, and the permute's in between) with
+    the node-by-node values, once; clearing or zeroing it drops the recipe,
+    and the next backward replaces it."""
+    from oxitorch_amd import _native
+    from oxitorch_amd.nn import functional as F
+    say("graph fusion: deferred intermediate gradient")
+    x, w, b, g = _inputs((4, 64, 768), 25)
+
+    def run(fuse, read_twice=False):
+        prev = _native.set_fuse_norm_act(fuse)
+        try:
+            tx, tw, tb = (ox.from_numpy(a, True) for a in (x, w, b))
+            h = F.layer_norm(tx, tw, tb)
+            hp = h.permute([0, 2, 1])
+            y = F.silu(hp)
+            y.backward(ox.from_numpy(g.transpose(0, 2, 1).copy()))
+            out = {"x": tx.grad.numpy(), "hp": hp.grad.numpy(), "h": h.grad.numpy()}
+            if read_twice:
+                assert np.array_equal(h.grad.numpy(), out["h"]) and np.array_equal(hp.grad.numpy(), out["hp"])
+                h.grad = None
+                assert h.grad is None
+                hp.zero_grad()
+                assert not hp.grad.numpy().any()
+            return out
+        finally:
+            _native.set_fuse_norm_act(prev)
+
+    before = _native.fused_norm_act_passes()
+    fused = run(True, read_twice=True)
+    assert _native.fused_norm_act_passes() - before == 1
+    plain = run(False)
+    for k in ("x", "hp", "h"):
+        assert np.array_equal(fused[k].view(np.uint32), plain[k].view(np.uint32)), k
+
+
 def test_graph_fusion_frees_both_vjps(ox):
     from oxitorch_amd import _native
     from oxitorch_amd.nn import functional as F
@@ -405,6 +452,7 @@ def _c5_chain(ox, F, fuse, B, T, H, V, seed):
         passes = _native.fused_norm_act_passes() - n0
         out = {"y": y.numpy(), "W": W.grad.numpy(), "lnw": LW.grad.numpy(), "lnb": LB.grad.numpy(),
                "rw": RW.grad.numpy(), "pos": P.grad.numpy(), "dn": n.grad.numpy(), "n": n.numpy(),
+               "dh": h.grad.numpy(),
                "rw_value": rw}
         return out, passes
     finally:
@@ -423,7 +471,7 @@ def test_c5_graph_fusions(ox, dims):
     fused, passes = _c5_chain(ox, F, True, B, T, H, 5000, 41)
     plain, none = _c5_chain(ox, F, False, B, T, H, 5000, 41)
     assert passes == 2 and none == 0, (passes, none)
-    for k in ("y", "W", "lnw", "lnb", "pos", "dn"):
+    for k in ("y", "W", "lnw", "lnb", "pos", "dn", "dh"):
         a, b = fused[k], plain[k]
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{dims}: {k} differs"
     # drw = sum over rows of dn * xhat (xhat = n / rw): both sums hold the same
