@@ -15,11 +15,14 @@ GPT-2 small's parameters) time the rows after the path.
 A config's step is the launch sequence the host core runs by default: with
 the graph fusions on, C2's backward is one layer_norm+gelu VJP pass and C5's
 is two fused passes (rms_norm+softmax with the positional gradient,
-layer_norm+silu through the permute). `gbs` divides the metric's per-op
-algorithmic bytes (every F.* op reading its inputs and writing its outputs
-once) by that step's time; `moved_gbs` divides the bytes the default step
-must move. The `unfused` block times the node-by-node sequence (the host
-core with OXI_FUSE_NORM_ACT=0).
+layer_norm+silu through the permute), none of which writes the norm output's
+gradient (the host core forms it if its .grad is read); C3's forward also
+writes the gradient for loss.backward()'s seed 1, so its backward launches
+nothing. `gbs` divides the metric's per-op algorithmic bytes (every F.* op
+reading its inputs and writing its outputs once) by that step's time;
+`moved_gbs` divides the bytes the default step must move, the figure to hold
+against the HBM peak. The `unfused` block times the step without those
+fusions (the host core with OXI_FUSE_NORM_ACT=0, or C3 with another seed).
 
 value = algorithmic bytes per step / time per step (GB/s). Algorithmic bytes
 are the per-op minimum (each op reads its inputs once and writes its outputs
@@ -40,8 +43,8 @@ Per config:
 - cold_cache: median of 20 steps each timed after a 512 MiB fill;
 - cpu_baseline: the CPU oracle (oracle/refcpu.c, a C restatement of the
   reference CPU path) on a bounded sample of the same workload on this host;
-- unfused (C2, C5): the node-by-node step;
-- dropin (C1, C2, C5): the same step through the Python surface
+- unfused (C2, C3, C5): the step without the host core's fusions;
+- dropin (C1, C2, C3, C5): the same step through the Python surface
   (F.* and backward() over the host core's graph), with its host time.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
@@ -289,13 +292,38 @@ class C3(Workload):
         self.loss, self.lse, self.d = A((1,)), A((n,)), A((n, c))
         self.bytes_per_step = 3 * n * c * 4
 
-    def kernels(self):
+    unfused_what = ("oxi_cross_entropy_fwd, then oxi_cross_entropy_bwd: the host core's path for any upstream "
+                    "gradient other than backward()'s implicit seed 1")
+
+    def unfused_kernels(self):
         L, c, n, C = self.hip.lib, self.hip.check, self.n, self.c
         E4 = n * C * 4
         return [("cross_entropy_fwd", lambda: c(L.oxi_cross_entropy_fwd(self.logits.ptr, self.t.ptr, self.loss.ptr,
                                                                         self.lse.ptr, n, C)), E4),
                 ("cross_entropy_bwd", lambda: c(L.oxi_cross_entropy_bwd(self.logits.ptr, self.t.ptr, self.lse.ptr,
                                                                         self.gl.ptr, self.d.ptr, n, C)), 2 * E4)]
+
+    # The host core's default for loss.backward(): the forward pass holds each
+    # row in registers and also writes the gradient for the seed 1, so the
+    # step reads the logits once and writes dlogits once (moved bytes 2 E),
+    # against the per-op count of 3 E the metric is defined on.
+    def kernels(self):
+        L, c, n, C = self.hip.lib, self.hip.check, self.n, self.c
+        E4 = n * C * 4
+        return [("cross_entropy_fwd_grad", lambda: c(L.oxi_cross_entropy_fwd_grad(
+            self.logits.ptr, self.t.ptr, self.loss.ptr, self.lse.ptr, self.d.ptr, n, C)), 2 * E4)]
+
+    dropin_what = "logits.grad = None; F.cross_entropy(logits, targets).backward(), targets a numpy int64 array"
+
+    def dropin(self, ox, F):
+        h = self.host
+        x = ox.from_numpy(h["logits"], True)
+        t = h["t"]
+
+        def step():
+            x.grad = None
+            F.cross_entropy(x, t).backward()
+        return step
 
     def cpu_step(self, ref, lo, hi):
         h = self.host
@@ -956,6 +984,7 @@ def run_config(hip, key, args):
         "launched": "the host core's default launch sequence (graph fusions on); gbs counts the per-op bytes",
         "moved_bytes_per_step": sum(b for _, _, b in kernels),
         "moved_gbs": round(sum(b for _, _, b in kernels) / (ms * 1e-3) / 1e9, 2),
+        "moved_pct_of_peak": round(100.0 * sum(b for _, _, b in kernels) / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
         "host_issue_ms_per_step": round(host_ms[0], 5),
         "kernels": _calls_json(per),
         "roofline": roofline(per, traffic, f"profiles/pmc_traffic_{key}.md"),
@@ -1052,6 +1081,13 @@ def main():
                    "rows_per_step": head["rows_per_step"],
                    "algorithmic_bytes_per_step": head["algorithmic_bytes_per_step"]},
         "pct_of_peak": head["pct_of_peak"],
+        "moved_gbs": head["moved_gbs"],
+        "moved_pct_of_peak": head["moved_pct_of_peak"],
+        "gbs_definitions": ("value/gbs/pct_of_peak: the metric's per-op algorithmic bytes (each F.* op reading its "
+                            "inputs and writing its outputs once) over the step's time, the rate a step of separate "
+                            "ops would need; it passes the HBM peak where the fused passes remove traffic. "
+                            "moved_gbs/moved_pct_of_peak: the bytes the step's kernels must move over the same time, "
+                            "the figure to hold against the 8 TB/s peak; roofline: the dominant kernel alone"),
         "rows_per_s": head["rows_per_s"],
         "roofline": head["roofline"],
         "cpu_baseline": head["cpu_baseline"],

@@ -317,6 +317,15 @@ int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets,
  * device pointer to the upstream scalar gradient. */
 int oxi_cross_entropy_bwd(const float* logits, const int64_t* targets, const float* lse,
                           const float* gloss, float* dlogits, int64_t n, int64_t c);
+/* oxi_cross_entropy_fwd and oxi_cross_entropy_bwd for gloss = 1 in one pass
+ * over the logits (no single reference counterpart: the composition of
+ * functional.py:277-293 and its VJPs, for a backward seeded with 1, as
+ * loss.backward() seeds it). Writes loss and lse as oxi_cross_entropy_fwd and
+ * dlogits as oxi_cross_entropy_bwd would with gloss[0] == 1, bit for bit.
+ * Needs c % 4 == 0 and 16-byte aligned logits and dlogits; other shapes
+ * return OXI_NOT_IMPLEMENTED before any launch (take the two calls then). */
+int oxi_cross_entropy_fwd_grad(const float* logits, const int64_t* targets, float* loss, float* lse,
+                               float* dlogits, int64_t n, int64_t c);
 
 /* ------------------------------------------------------------------------ */
 /* Gather / scatter-add.                                                     */

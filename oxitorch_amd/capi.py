@@ -95,6 +95,7 @@ _SIGS = {
     "oxi_log_softmax_bwd": [vp, vp, vp, c_i64, c_i64, c_i64],
     "oxi_cross_entropy_fwd": [vp, vp, vp, vp, c_i64, c_i64],
     "oxi_cross_entropy_bwd": [vp, vp, vp, vp, vp, c_i64, c_i64],
+    "oxi_cross_entropy_fwd_grad": [vp, vp, vp, vp, vp, c_i64, c_i64],
     "oxi_index_select": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
     "oxi_batch_gather": [vp, c_int, c_i64, vp, c_i64],
     "oxi_index_select_bwd": [vp, c_i64, c_i64, c_i64, vp, c_i64, vp],
@@ -435,6 +436,16 @@ def cross_entropy_fwd(logits: DeviceArray, targets: DeviceArray):
     lse = DeviceArray((n,))
     call("oxi_cross_entropy_fwd", logits.ptr, targets.ptr, loss.ptr, lse.ptr, n, c)
     return loss, lse
+
+
+def cross_entropy_fwd_grad(logits: DeviceArray, targets: DeviceArray):
+    """Loss, lse and the gradient for an upstream 1 in one pass (oxi_cross_entropy_fwd_grad)."""
+    n, c = logits.shape
+    loss = DeviceArray((1,))
+    lse = DeviceArray((n,))
+    d = DeviceArray((n, c))
+    call("oxi_cross_entropy_fwd_grad", logits.ptr, targets.ptr, loss.ptr, lse.ptr, d.ptr, n, c)
+    return loss, lse, d
 
 
 def cross_entropy_bwd(logits: DeviceArray, targets: DeviceArray, lse: DeviceArray, gloss: DeviceArray):

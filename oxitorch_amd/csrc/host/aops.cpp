@@ -6,6 +6,7 @@
 // Gradients produced inside VJPs keep the common dense layout of their
 // operands (result_strides): a gradient flowing through a permuted view stays
 // permuted, so the permute VJP hands the next node a contiguous tensor.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -593,12 +594,26 @@ Var cross_entropy(const Var& logits, const std::vector<int64_t>& targets) {
   require_hip(lv, "cross_entropy");
   Tensor lc = t_contiguous(lv);
   auto tg = device_i64(targets);
+  const int64_t* tp = static_cast<const int64_t*>(tg->ptr);
   Tensor loss = Tensor::empty({}, Dev::Hip);
   Tensor lse = Tensor::empty({n}, Dev::Hip);
-  hip_check(oxi_cross_entropy_fwd(lc.data(), static_cast<const int64_t*>(tg->ptr), loss.data(), lse.data(), n, c));
+  // With a gradient to come, the forward pass also forms the gradient for an
+  // upstream 1 (loss.backward()'s seed) from the logits it holds: the first
+  // backward seeded so takes it as is; any other upstream, or a second
+  // backward, runs the backward kernel.
+  std::optional<Tensor> unit;
+  if (logits.requires_grad() && is_grad_enabled()) {
+    Tensor d = Tensor::empty({n, c}, Dev::Hip);
+    const int rc = oxi_cross_entropy_fwd_grad(lc.data(), tp, loss.data(), lse.data(), d.data(), n, c);
+    if (rc == OXI_OK) unit = d;
+    else if (rc != OXI_NOT_IMPLEMENTED) hip_check(rc);
+  }
+  if (!unit) hip_check(oxi_cross_entropy_fwd(lc.data(), tp, loss.data(), lse.data(), n, c));
+  auto fresh = std::make_shared<std::atomic<bool>>(unit.has_value());
   return Var::op(loss, "cross_entropy", {logits},
-                 [lc, tg, lse, n, c](const Tensor& g, const std::vector<bool>& need) -> Grads {
+                 [lc, tg, lse, n, c, unit, fresh](const Tensor& g, const std::vector<bool>& need) -> Grads {
                    if (!need[0]) return {std::nullopt};
+                   if (is_implicit_seed(g) && fresh->exchange(false)) return {*unit};
                    Tensor gs = t_contiguous(g);
                    Tensor d = Tensor::empty({n, c}, Dev::Hip);
                    hip_check(oxi_cross_entropy_bwd(lc.data(), static_cast<const int64_t*>(tg->ptr), lse.data(),

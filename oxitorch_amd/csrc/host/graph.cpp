@@ -244,6 +244,18 @@ std::vector<std::optional<Tensor>> add_grads(const LeadSum& ls, const std::optio
 // - when the norm's input is r = p + q with q broadcast over the leading dim
 //   (a positional table) and r feeds nothing else, the norm pass also forms
 //   q's gradient (oxi_*_norm_bwd_lead_sum), held for the add node.
+namespace {
+thread_local const Storage* t_implicit_seed = nullptr;
+
+struct SeedScope {
+  const Storage* prev;
+  explicit SeedScope(const Storage* st) : prev(t_implicit_seed) { t_implicit_seed = st; }
+  ~SeedScope() { t_implicit_seed = prev; }
+};
+}  // namespace
+
+bool is_implicit_seed(const Tensor& g) { return g.st && g.st.get() == t_implicit_seed; }
+
 void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
   if (!root.requires_grad())
     err_invalid("element 0 of tensors does not require grad and does not have a grad_fn");
@@ -256,6 +268,7 @@ void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph) {
   } else {
     err_invalid("grad can be implicitly created only for scalar outputs; pass a seed tensor");
   }
+  SeedScope scope(seed ? nullptr : s.st.get());
   std::vector<Var> order = topo_order(root);
   for (Var& n : order)
     if (n.node->op) {

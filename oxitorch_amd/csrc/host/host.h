@@ -227,6 +227,9 @@ class Var {
 
 Tensor unbroadcast(const Tensor& g, const Shape& shape);
 void backward(const Var& root, std::optional<Tensor> seed, bool retain_graph);
+// Whether `g` is (a view of) the seed backward() made itself, ones
+// everywhere, in the backward pass now running on this thread.
+bool is_implicit_seed(const Tensor& g);
 // Whether backward runs norm + activation VJPs as one pass (OXI_FUSE_NORM_ACT,
 // default on; the setter overrides the environment and returns the old value).
 bool fuse_norm_act();

@@ -201,7 +201,9 @@ constexpr int CE_BS = 256;
 constexpr int CE_U = 4;   // forward: float4 loads in flight per thread per step
 constexpr int CE_BU = 1;  // backward: float4s per thread (one per thread streams fastest)
 
-// One block per row. lse[row] = max + log(sum exp(x - max));
+// Rows longer than the register-row kernel takes (more than 16384 float4s,
+// or not vectorizable): one block per row, streaming it.
+// lse[row] = max + log(sum exp(x - max));
 // picked[row] = (x[t] - max) - log(sum)  (the reference's ls[row, t]).
 __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logits, const int64_t* __restrict__ targets,
                                                   float* __restrict__ lse, float* __restrict__ picked, int64_t n, int C,
@@ -249,6 +251,75 @@ __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logi
     const float L = logf(o.s);
     lse[row] = o.m + L;
     picked[row] = (xr[t] - o.m) - L;
+  }
+}
+
+// Rows of up to RT * NV float4s, a row per block held in registers, so each
+// row crosses HBM once: the row max and the sum of exp(x - max) (two block
+// reductions), lse and picked. With `dunit` set the block also writes, from
+// the registers, the gradient of the mean loss for an upstream gradient of
+// exactly 1: (exp(x - lse) - onehot) * (1 / n), what ce_bwd_k writes for
+// gloss = 1, so a backward seeded with 1 has nothing left to compute.
+// Measured at C3 (8192 x 32000): 512 x 16 runs the forward with the gradient
+// in 380 us (1024 x 8, held to one block per CU by its 68 VGPRs: 476 us;
+// 256 x 32: 417 us) and the forward alone in 181 us (streaming: 174 us).
+template <int RT, int NV, bool NTS>
+__global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ logits,
+                                                    const int64_t* __restrict__ targets, float* __restrict__ lse,
+                                                    float* __restrict__ picked, float* __restrict__ dunit, int64_t n,
+                                                    int C, int* __restrict__ guard) {
+  __shared__ float lds[2 * (RT / 64)];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int c4 = C >> 2;
+  const float* xr = logits + row * C;
+  const f4* p = reinterpret_cast<const f4*>(xr);
+  f4 v[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int c = k * RT + t;
+    v[k] = c < c4 ? ld_stream(p + c) : f4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+  }
+  float m = NEG_INF;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) m = fmaxf(m, max4(v[k]));
+  m = group_max<RT>(m, lds);
+  const float ms = m == NEG_INF ? 0.f : m;
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    if (k * RT + t < c4) s += sum4(exp4(v[k] - ms));
+  s = group_sum<RT, float>(s, lds + RT / 64);
+  int64_t tg = targets[row];
+  if (tg < 0 || tg >= C) {
+    if (t == 0) atomicOr(guard, 1);
+    tg = 0;
+  }
+  const float L = logf(s);
+  const float l = m + L;
+  if (t == 0) {
+    lse[row] = l;
+    picked[row] = (xr[tg] - m) - L;
+  }
+  if (dunit) {
+    const float scale = 1.0f / (float)n;
+    f4* q = reinterpret_cast<f4*>(dunit + row * C);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c = k * RT + t;
+      if (c < c4) {
+        f4 e = exp4(v[k] - l);
+        const int64_t base = (int64_t)c * 4;
+        if (tg >= base && tg < base + 4) {
+          const int j = (int)(tg - base);
+          if (j == 0) e.x -= 1.f;
+          else if (j == 1) e.y -= 1.f;
+          else if (j == 2) e.z -= 1.f;
+          else e.w -= 1.f;
+        }
+        st_stream<NTS>(e * scale, q + c);
+      }
+    }
   }
 }
 
@@ -442,23 +513,73 @@ int oxi_log_softmax_bwd(const float* y, const float* g, float* dx, int64_t outer
   return launch_bwd<true>(y, g, dx, outer, len, inner);
 }
 
-int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets, float* loss, float* lse, int64_t n, int64_t c) {
-  if (n < 0 || c < 0) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: negative size");
-  if (!loss) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: loss must not be NULL");
+}  // extern "C"
+
+namespace oxi {
+namespace {
+
+// Loss and lse; with `dunit`, also the gradient for an upstream 1 (rows of
+// c % 4 == 0 with 16-byte aligned operands only: NOT_IMPLEMENTED otherwise,
+// before anything is launched).
+int ce_forward(const char* what, const float* logits, const int64_t* targets, float* loss, float* lse, float* dunit,
+               int64_t n, int64_t c) {
+  if (n < 0 || c < 0) return fail(OXI_INVALID_ARGUMENT, "%s: negative size", what);
+  if (!loss) return fail(OXI_INVALID_ARGUMENT, "%s: loss must not be NULL", what);
   if (c > ((int64_t)1 << 30) || n > ((int64_t)1 << 31) - 1)
-    return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: size exceeds the kernel limits");
+    return fail(OXI_INVALID_ARGUMENT, "%s: size exceeds the kernel limits", what);
   OXI_CHECK_INIT();
   if (n == 0) return oxi_fill(loss, 1, __builtin_nanf(""));  // mean of nothing (Tensor::mean_all, lib.rs:589-593)
-  if (c == 0) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: zero classes");
-  if (!logits || !targets || !lse) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd: NULL tensor pointer");
+  if (c == 0) return fail(OXI_INVALID_ARGUMENT, "%s: zero classes", what);
+  if (!logits || !targets || !lse) return fail(OXI_INVALID_ARGUMENT, "%s: NULL tensor pointer", what);
+  const int vec = (c % 4 == 0 && aligned16({logits})) ? 1 : 0;
+  const int64_t c4 = c / 4;
+  // (threads, float4s a thread) of the register-row kernel: 16 float4s a
+  // thread, as few threads as the row needs
+  int rt = 0;
+  if (vec) rt = c4 <= 1024 ? 64 : c4 <= 2048 ? 128 : c4 <= 4096 ? 256 : c4 <= 8192 ? 512 : c4 <= 16384 ? 1024 : 0;
+  if (dunit && !(rt && aligned16({dunit})))
+    return fail(OXI_NOT_IMPLEMENTED, "%s: rows of %lld classes do not take the one-pass kernel (c %% 4 != 0, more "
+                "than 65536 classes or unaligned)", what, (long long)c);
   Workspace picked(sizeof(float) * (size_t)n);
   if (!picked.p) return fail_alloc("cross_entropy_fwd: workspace");
-  const int vec = (c % 4 == 0 && aligned16({logits})) ? 1 : 0;
-  ce_fwd_k<<<dim3((unsigned)n), dim3(CE_BS), 0, stream()>>>(logits, targets, lse, picked.as<float>(), n, (int)c, vec,
-                                                            guard_flag());
-  if (int rc = check_launch("cross_entropy_fwd")) return rc;
+  const dim3 grid((unsigned)n);
+  float* pk = picked.as<float>();
+  const bool nt = nt_stores(n * c * 4);
+  switch (rt) {
+#define OXI_CE_ROWS(RT)                                                                                     \
+  case RT:                                                                                                  \
+    if (nt) ce_fwd_rows_k<RT, 16, true><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, (int)c, \
+                                                                         guard_flag());                     \
+    else ce_fwd_rows_k<RT, 16, false><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, (int)c, \
+                                                                       guard_flag());                       \
+    break;
+    OXI_CE_ROWS(64)
+    OXI_CE_ROWS(128)
+    OXI_CE_ROWS(256)
+    OXI_CE_ROWS(512)
+    OXI_CE_ROWS(1024)
+#undef OXI_CE_ROWS
+    default:
+      ce_fwd_k<<<grid, dim3(CE_BS), 0, stream()>>>(logits, targets, lse, pk, n, (int)c, vec, guard_flag());
+  }
+  if (int rc = check_launch(what)) return rc;
   ce_mean_k<<<1, 1024, 0, stream()>>>(picked.as<float>(), n, loss);
   return check_launch("cross_entropy_mean");
+}
+
+}  // namespace
+}  // namespace oxi
+
+extern "C" {
+
+int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets, float* loss, float* lse, int64_t n, int64_t c) {
+  return ce_forward("cross_entropy_fwd", logits, targets, loss, lse, nullptr, n, c);
+}
+
+int oxi_cross_entropy_fwd_grad(const float* logits, const int64_t* targets, float* loss, float* lse, float* dlogits,
+                               int64_t n, int64_t c) {
+  if (!dlogits && n > 0 && c > 0) return fail(OXI_INVALID_ARGUMENT, "cross_entropy_fwd_grad: NULL dlogits");
+  return ce_forward("cross_entropy_fwd_grad", logits, targets, loss, lse, n > 0 && c > 0 ? dlogits : nullptr, n, c);
 }
 
 int oxi_cross_entropy_bwd(const float* logits, const int64_t* targets, const float* lse, const float* gloss,

@@ -113,6 +113,42 @@ def test_cross_entropy_value_and_grad(ox, F):
     assert np.allclose(logits.grad.numpy(), g, rtol=1e-4, atol=1e-6)
 
 
+@pytest.mark.parametrize("c", [1000, 32000, 50257])
+def test_cross_entropy_seeded_with_one_takes_the_forward_gradient(ox, F, c):
+    """loss.backward() (the implicit seed 1) hands the logits the gradient
+    the forward pass formed; an explicit seed, a loss used inside the graph,
+    a retained second backward and rows whose class count is not a multiple
+    of 4 all run the backward kernel, with the same bits (twice the gradient when
+    doubled, which is exact in binary)."""
+    say("cross_entropy backward seeds", c)
+    r = np.random.default_rng(c)
+    n = 16
+    la = (r.standard_normal((n, c), dtype=np.float32) * 2).astype(np.float32)
+    t = r.integers(0, c, n)
+
+    def grad_of(run):
+        x = _t(ox, la, True)
+        run(x)
+        return x.grad.numpy()
+
+    implicit = grad_of(lambda x: F.cross_entropy(x, t).backward())
+    explicit = grad_of(lambda x: F.cross_entropy(x, t).backward(ox.from_numpy(np.ones((), np.float32))))
+    doubled = grad_of(lambda x: (F.cross_entropy(x, t) * 2.0).backward())
+
+    def twice(x):
+        loss = F.cross_entropy(x, t)
+        loss.backward(retain_graph=True)
+        loss.backward()
+    both = grad_of(twice)
+    assert np.array_equal(implicit.view(np.uint32), explicit.view(np.uint32))
+    assert np.array_equal((2 * implicit).view(np.uint32), doubled.view(np.uint32))
+    assert np.array_equal((2 * implicit).view(np.uint32), both.view(np.uint32))
+    m = la.max(-1, keepdims=True)
+    ls = la - m - np.log(np.exp(la - m).sum(-1, keepdims=True))
+    want = (np.exp(ls) - np.eye(c, dtype=np.float32)[t]) / n
+    assert np.allclose(implicit, want, rtol=1e-4, atol=1e-6)
+
+
 def test_cross_entropy_rejects_wrong_batch(ox, F):
     with pytest.raises(ValueError, match="targets"):
         F.cross_entropy(_t(ox, np.zeros((2, 3))), [0, 1, 2])

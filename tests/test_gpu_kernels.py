@@ -249,6 +249,40 @@ def test_cross_entropy(hip, n, c):
                      what="n*dlogits")
 
 
+@pytest.mark.parametrize("n,c", [(2, 4), (64, 1000), (7, 36), (33, 8196), (256, 32000), (5, 65536), (3, 4100),
+                                 (9, 8192), (4, 16388), (8192, 32000)])
+def test_cross_entropy_fwd_grad_is_fwd_then_bwd(hip, n, c):
+    """The forward that also writes the gradient for an upstream 1 writes the
+    loss and lse of oxi_cross_entropy_fwd and the dlogits of
+    oxi_cross_entropy_bwd(gloss = 1), bit for bit (every block width of the
+    register-row kernel and both sides of each width's limit, C3 included)."""
+    say("cross_entropy_fwd_grad", n, c)
+    r = rng(n + c)
+    logits = (r.standard_normal((n, c), dtype=np.float32) * 3).astype(np.float32)
+    t = r.integers(0, c, n).astype(np.int64)
+    t[0] = c - 1
+    dl, dt = D(hip, logits), D(hip, t)
+    loss, lse = hip.cross_entropy_fwd(dl, dt)
+    d = hip.cross_entropy_bwd(dl, dt, lse, D(hip, np.ones(1, np.float32)))
+    loss2, lse2, d2 = hip.cross_entropy_fwd_grad(dl, dt)
+    for a, b, what in ((loss2, loss, "loss"), (lse2, lse, "lse"), (d2, d, "dlogits")):
+        a, b = a.numpy(), b.numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"({n}, {c}) {what} differs"
+
+
+def test_cross_entropy_fwd_grad_refusals(hip):
+    """Rows past 65536 classes or of a class count that is not a multiple of
+    4 are refused before any launch (the two-call path serves them)."""
+    say("cross_entropy_fwd_grad refusals")
+    for n, c in ((3, 65540), (3, 50257), (4, 10)):
+        dl = D(hip, np.zeros((n, c), np.float32))
+        dt = D(hip, np.zeros(n, np.int64))
+        with pytest.raises(NotImplementedError, match="do not take the one-pass kernel"):
+            hip.cross_entropy_fwd_grad(dl, dt)
+        loss, _ = hip.cross_entropy_fwd(dl, dt)
+        assert np.isclose(float(loss.numpy()[0]), np.log(c), rtol=1e-6)
+
+
 def test_cross_entropy_c3_full(hip):
     """Config 3 at full size (8192, 32000): loss vs float64 over all rows, grads on a row sample."""
     from oracle import ref, closed_form
