@@ -756,12 +756,15 @@ def time_steps(hip, kernels, steps, host=None):
 
 
 def time_calls(hip, kernels, reps):
-    """Each C-ABI call of the step timed alone: one untimed launch, then
-    `reps` back-to-back launches between two events on the library stream.
-    The average includes no event records between launches."""
+    """Each C-ABI call of the step timed alone: two untimed launches (a
+    repeated call can take a path the first does not, e.g. a plan applied a
+    second time, and a kernel's first launch loads its code), then `reps`
+    back-to-back launches between two events on the library stream. The
+    average includes no event records between launches."""
     t = hip.Timer()
     out = {}
     for label, fn, nbytes in kernels:
+        fn()
         fn()
         hip.sync()
         t.start()

@@ -413,7 +413,14 @@ __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict_
 // Blocks past the segment work write zero rows for keys that never occur
 // (ZR rows per block), so those writes overlap the gathers.
 
-constexpr int SEG_U = 8;  // rows in flight per lane
+// Rows in flight per lane, and the longest segment tile (below). Measured on
+// C4 (131072 Zipf ids, 1024-float rows), C4 step: 8 and 64 take 252 us;
+// 4 rows 264 us, 32-position tiles 259 us, 16 or 32 rows (the accumulation
+// loop no longer unrolls) 440-463 us.
+#ifndef OXI_SEG_U
+#define OXI_SEG_U 8
+#endif
+constexpr int SEG_U = OXI_SEG_U;
 constexpr int ZR = 4;
 
 template <bool VEC, bool NTS>
@@ -746,7 +753,10 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   const int64_t chunks = ceil_div(units, 64);
   const int64_t c16 = ceil_div(units, 16);
   if (c16 >= (1 << 24)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: rows too wide");
-  int st = 64;
+#ifndef OXI_SEG_ST
+#define OXI_SEG_ST 64
+#endif
+  int st = OXI_SEG_ST;
   while (st > 16 && ceil_div(n, st) * chunks < 8 * (int64_t)cu_count()) st >>= 1;
   const int64_t stiles = ceil_div(n, st);
   // end tile per key and the owner list of long keys; partial rows
