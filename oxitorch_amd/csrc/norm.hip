@@ -239,8 +239,11 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM>())) void norm_bwd_k(con
   auto slot = [&]() { return lds + ((red++ & 1) ? NT / 64 : 0); };
   auto fetch = [&](RowTile<TPR, NV>& xt, RowTile<TPR, NV>& gt, float& inv, float& mu, int64_t r) {
     r = r < rows ? r : rows - 1;
-    xt.load_clamped(x + r * H, h4, t);
-    gt.load_clamped(g + r * H, h4, t);
+    // the lead-sum walk's last refills re-read a row it has just read: plain
+    // loads keep it in L2 (non-temporal ones fetched it from HBM again, +25%
+    // reads at 16 rows a position)
+    xt.template load_clamped<!LSUM>(x + r * H, h4, t);
+    gt.template load_clamped<!LSUM>(g + r * H, h4, t);
     inv = rstd[r];
     if constexpr (LN) mu = mean[r];
   };
@@ -373,7 +376,7 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM>())) void norm_bwd_k(con
     // the leading dim, bit for bit. No barriers. lead is a multiple of
     // LSUM_DEPTH (the host checks), so every round processes LSUM_DEPTH rows
     // and every refill load issues: the waits count exactly the younger
-    // loads. The last round's refills re-read the wave's last row (cache).
+    // loads. The last round's refills re-read the wave's last row (from L2).
     const int lead = (int)(rows / T);
     const int waves = (int)gridDim.x * GPB;
     const int wave = (int)blockIdx.x * GPB + gi;

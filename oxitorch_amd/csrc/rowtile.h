@@ -86,10 +86,16 @@ struct RowTile {
   }
   // Every lane loads: lanes past the row (c >= h4) re-read its last float4,
   // so the loads issue unconditionally; the caller zeroes those lanes at use.
+  // NT = false: plain loads, for rows the caller reads again soon.
+  template <bool NT = true>
   __device__ __forceinline__ void load_clamped(const float* __restrict__ row, int h4, int t) {
     const f4* p = reinterpret_cast<const f4*>(row);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) v[k] = ld_stream(p + min(k * TPR + t, h4 - 1));
+    for (int k = 0; k < NV; ++k) {
+      const f4* q = p + min(k * TPR + t, h4 - 1);
+      if constexpr (NT) v[k] = ld_stream(q);
+      else v[k] = *q;
+    }
   }
   template <bool NT>
   __device__ __forceinline__ void store(float* __restrict__ row, int h4, int t) const {

@@ -263,7 +263,7 @@ __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logi
 // Measured at C3 (8192 x 32000): 512 x 16 runs the forward with the gradient
 // in 380 us (1024 x 8, held to one block per CU by its 68 VGPRs: 476 us;
 // 256 x 32: 417 us) and the forward alone in 181 us (streaming: 174 us).
-template <int RT, int NV, bool NTS>
+template <int RT, int NV, bool GRAD, bool NTS>
 __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ logits,
                                                     const int64_t* __restrict__ targets, float* __restrict__ lse,
                                                     float* __restrict__ picked, float* __restrict__ dunit, int64_t n,
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
     lse[row] = l;
     picked[row] = (xr[tg] - m) - L;
   }
-  if (dunit) {
+  if constexpr (GRAD) {
     const float scale = 1.0f / (float)n;
     f4* q = reinterpret_cast<f4*>(dunit + row * C);
 #pragma unroll
@@ -544,14 +544,19 @@ int ce_forward(const char* what, const float* logits, const int64_t* targets, fl
   if (!picked.p) return fail_alloc("cross_entropy_fwd: workspace");
   const dim3 grid((unsigned)n);
   float* pk = picked.as<float>();
-  const bool nt = nt_stores(n * c * 4);
+  const bool nt = nt_stores(n * c * 4);  // the gradient's stores
   switch (rt) {
 #define OXI_CE_ROWS(RT)                                                                                     \
   case RT:                                                                                                  \
-    if (nt) ce_fwd_rows_k<RT, 16, true><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, (int)c, \
-                                                                         guard_flag());                     \
-    else ce_fwd_rows_k<RT, 16, false><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, (int)c, \
-                                                                       guard_flag());                       \
+    if (!dunit)                                                                                             \
+      ce_fwd_rows_k<RT, 16, false, false><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, nullptr, n, \
+                                                                           (int)c, guard_flag());           \
+    else if (nt)                                                                                            \
+      ce_fwd_rows_k<RT, 16, true, true><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, \
+                                                                         (int)c, guard_flag());             \
+    else                                                                                                    \
+      ce_fwd_rows_k<RT, 16, true, false><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, \
+                                                                          (int)c, guard_flag());            \
     break;
     OXI_CE_ROWS(64)
     OXI_CE_ROWS(128)
