@@ -18,16 +18,19 @@ is two fused passes (rms_norm+softmax with the positional gradient,
 layer_norm+silu through the permute), none of which writes the norm output's
 gradient (the host core forms it if its .grad is read); C3's forward also
 writes the gradient for loss.backward()'s seed 1, so its backward launches
-nothing. `gbs` divides the metric's per-op algorithmic bytes (every F.* op
-reading its inputs and writing its outputs once) by that step's time;
-`moved_gbs` divides the bytes the default step must move, the figure to hold
-against the HBM peak. The `unfused` block times the step without those
-fusions (the host core with OXI_FUSE_NORM_ACT=0, or C3 with another seed).
+nothing. `gbs` (and the headline `value`) divides the HBM bytes the step's
+kernels must move (each call's reads and writes; C4's gather counted as
+reading each distinct row of W once; checked against the PMC counters in
+profiles/pmc_traffic_<config>.md) by the step's time, against the 8 TB/s
+peak. `per_op_gbs` divides the metric's per-op algorithmic bytes (every F.*
+op reading its inputs and writing its outputs once) by the same time: the
+rate a step of separate ops would need, which passes the peak where the
+fused passes remove traffic. The `unfused` block times the step without
+those fusions (the host core with OXI_FUSE_NORM_ACT=0, or C3 with another
+seed).
 
-value = algorithmic bytes per step / time per step (GB/s). Algorithmic bytes
-are the per-op minimum (each op reads its inputs once and writes its outputs
-once). Time per step comes from HIP events recorded on the library stream
-(the stream every liboxihip kernel runs on) around K back-to-back steps.
+Time per step comes from HIP events recorded on the library stream (the
+stream every liboxihip kernel runs on) around K back-to-back steps.
 
 Per config:
 - kernels: each C-ABI call of the step timed alone over back-to-back
@@ -360,8 +363,9 @@ class C4(Workload):
         L, c = self.hip.lib, self.hip.check
         ep = self.emb = getattr(self, "emb", None) or EmbeddingPlan(self.hip)
         return [("embedding_bwd_plan", lambda: ep.plan_sort(self.ids.ptr, self.n, self.V), 0),
+                # HBM bytes: each distinct row of W once (repeats come from the caches)
                 ("embedding_fwd", lambda: ep.forward(self.W.ptr, self.ids.ptr, self.n, self.V, self.Dm,
-                                                     self.out.ptr), self.fwd_bytes),
+                                                     self.out.ptr), self.fwd_bytes_unique),
                 ("embedding_bwd", lambda: ep.backward(self.g.ptr, self.Dm, self.dW.ptr), self.bwd_bytes)]
 
     def cpu_step(self, ref, lo, hi):
@@ -929,7 +933,7 @@ def roofline(per, traffic, source):
             "avg_launch_ms": round(d["ms"], 5), "timing": "back-to-back launches of the call alone"}
 
 
-def time_dropin(hip, wl, steps, warmup):
+def time_dropin(hip, wl, steps, warmup, hbm):
     """The step through the Python surface (F.* and backward() over the host
     core's graph): device time per step (events on the library stream around
     `steps` steps, so host gaps count) and the host's time per step."""
@@ -957,7 +961,7 @@ def time_dropin(hip, wl, steps, warmup):
     ms = t.stop() / steps
     hip.sync()
     return {"what": wl.dropin_what, "steps": steps, "ms_per_step": round(ms, 5),
-            "host_ms_per_step": round((h1 - h0) * 1e3 / steps, 5), "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 2)}
+            "host_ms_per_step": round((h1 - h0) * 1e3 / steps, 5), "gbs": round(hbm / (ms * 1e-3) / 1e9, 2)}
 
 
 def run_config(hip, key, args):
@@ -974,7 +978,9 @@ def run_config(hip, key, args):
     ms = time_steps(hip, kernels, args.steps, host_ms)
     reps = max(5, min(args.steps, 20))
     per = time_calls(hip, kernels, reps)
-    gbs = wl.bytes_per_step / (ms * 1e-3) / 1e9
+    hbm = sum(b for _, _, b in kernels)
+    gbs = hbm / (ms * 1e-3) / 1e9
+    per_op = wl.bytes_per_step / (ms * 1e-3) / 1e9
     traffic = pmc_traffic(key)
     block = {
         "workload": wl.name,
@@ -983,23 +989,17 @@ def run_config(hip, key, args):
         "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
         "rows_per_step": wl.rows,
         "rows_per_s": round(wl.rows / (ms * 1e-3), 1),
-        "algorithmic_bytes_per_step": wl.bytes_per_step,
-        "launched": "the host core's default launch sequence (graph fusions on); gbs counts the per-op bytes",
-        "moved_bytes_per_step": sum(b for _, _, b in kernels),
-        "moved_gbs": round(sum(b for _, _, b in kernels) / (ms * 1e-3) / 1e9, 2),
-        "moved_pct_of_peak": round(100.0 * sum(b for _, _, b in kernels) / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+        "hbm_bytes_per_step": hbm,
+        "launched": "the host core's default launch sequence (graph fusions on)",
+        "per_op_bytes_per_step": wl.bytes_per_step,
+        "per_op_gbs": round(per_op, 2),
+        "per_op_pct_of_peak": round(100.0 * per_op / PEAK_HBM_GBS, 2),
         "host_issue_ms_per_step": round(host_ms[0], 5),
         "kernels": _calls_json(per),
         "roofline": roofline(per, traffic, f"profiles/pmc_traffic_{key}.md"),
     }
     if isinstance(wl, C4):
-        mu = wl.fwd_bytes_unique + wl.bwd_bytes
-        block["unique_rows"] = {
-            "distinct_ids": wl.unique_rows, "algorithmic_bytes_per_step": mu,
-            "gbs": round(mu / (ms * 1e-3) / 1e9, 2), "pct_of_peak": round(100.0 * mu / (ms * 1e-3) / 1e9 /
-                                                                           PEAK_HBM_GBS, 2),
-            "embedding_fwd_gbs": round(wl.fwd_bytes_unique / (per["embedding_fwd"]["ms"] * 1e-3) / 1e9, 1),
-            "what": "the forward gather counted as reading each distinct row of W once"}
+        block["distinct_ids"] = wl.unique_rows  # the rows of W the gather's HBM bytes count
     if hasattr(wl, "unfused_kernels"):
         uk = wl.unfused_kernels()
         for _ in range(max(args.warmup, 1)):
@@ -1022,7 +1022,7 @@ def run_config(hip, key, args):
         log(f"[{key}] cold-cache median")
         ms_cold = time_cold(hip, kernels)
         block["cold_cache"] = {"ms_per_step_median_of_20": round(ms_cold, 5),
-                               "gbs": round(wl.bytes_per_step / (ms_cold * 1e-3) / 1e9, 2),
+                               "gbs": round(hbm / (ms_cold * 1e-3) / 1e9, 2),
                                "protocol": "512 MiB fill before each timed step"}
     if hasattr(wl, "side_figures"):
         block["pcie_gbs"] = wl.side_figures()
@@ -1033,7 +1033,7 @@ def run_config(hip, key, args):
                                         "gbs": round(wl.bytes_per_step / (ms_alt * 1e-3) / 1e9, 2)}
     if hasattr(wl, "dropin") and not args.no_dropin:
         log(f"[{key}] timing the F.*/backward() step")
-        d = time_dropin(hip, wl, max(3, min(args.steps, 10)), args.warmup)
+        d = time_dropin(hip, wl, max(3, min(args.steps, 10)), args.warmup, hbm)
         d["vs_capi_ms_per_step"] = block["ms_per_step"]
         d["overhead_pct"] = round(100.0 * (d["ms_per_step"] / block["ms_per_step"] - 1.0), 1)
         block["dropin"] = d
@@ -1082,15 +1082,17 @@ def main():
                    "why": ("the largest config (3.15 GB per step); every config's block is under configs"
                            if args.config == "all" else "selected with --config"),
                    "rows_per_step": head["rows_per_step"],
-                   "algorithmic_bytes_per_step": head["algorithmic_bytes_per_step"]},
+                   "hbm_bytes_per_step": head["hbm_bytes_per_step"],
+                   "per_op_bytes_per_step": head["per_op_bytes_per_step"]},
         "pct_of_peak": head["pct_of_peak"],
-        "moved_gbs": head["moved_gbs"],
-        "moved_pct_of_peak": head["moved_pct_of_peak"],
-        "gbs_definitions": ("value/gbs/pct_of_peak: the metric's per-op algorithmic bytes (each F.* op reading its "
-                            "inputs and writing its outputs once) over the step's time, the rate a step of separate "
-                            "ops would need; it passes the HBM peak where the fused passes remove traffic. "
-                            "moved_gbs/moved_pct_of_peak: the bytes the step's kernels must move over the same time, "
-                            "the figure to hold against the 8 TB/s peak; roofline: the dominant kernel alone"),
+        "per_op_gbs": head["per_op_gbs"],
+        "per_op_pct_of_peak": head["per_op_pct_of_peak"],
+        "gbs_definitions": ("value/gbs/pct_of_peak: the HBM bytes the step's kernels move (per C-ABI call, checked "
+                            "against rocprofv3 FETCH_SIZE + WRITE_SIZE in profiles/pmc_traffic_<config>.md) over "
+                            "the step's time, against the 8 TB/s peak. per_op_gbs/per_op_pct_of_peak: the per-op "
+                            "algorithmic bytes of BASELINE.md (each F.* op reading its inputs and writing its "
+                            "outputs once) over the same time, the rate a step of separate ops would need; it passes "
+                            "the peak where the fused passes remove traffic. roofline: the dominant call alone"),
         "rows_per_s": head["rows_per_s"],
         "roofline": head["roofline"],
         "cpu_baseline": head["cpu_baseline"],
