@@ -320,9 +320,12 @@ int oxi_cross_entropy_bwd(const float* logits, const int64_t* targets, const flo
 /* oxi_cross_entropy_fwd and oxi_cross_entropy_bwd for gloss = 1 in one pass
  * over the logits (no single reference counterpart: the composition of
  * functional.py:277-293 and its VJPs, for a backward seeded with 1, as
- * loss.backward() seeds it). Writes loss and lse as oxi_cross_entropy_fwd and
- * dlogits as oxi_cross_entropy_bwd would with gloss[0] == 1, bit for bit.
- * Needs c % 4 == 0 and 16-byte aligned logits and dlogits; other shapes
+ * loss.backward() seeds it). Writes loss and lse as oxi_cross_entropy_fwd
+ * does, bit for bit, and dlogits as the composed log_softmax VJP forms them:
+ * (1/n)(1/s) exp(x - max) with s the row's sum of exp(x - max), less 1/n at
+ * the target (oxi_cross_entropy_bwd, which has only lse, writes
+ * (exp(x - lse) - onehot)/n; the two agree to within the reference path's
+ * tolerance, not bit for bit). Needs c % 4 == 0 and 16-byte aligned logits and dlogits; other shapes
  * return OXI_NOT_IMPLEMENTED before any launch (take the two calls then). */
 int oxi_cross_entropy_fwd_grad(const float* logits, const int64_t* targets, float* loss, float* lse,
                                float* dlogits, int64_t n, int64_t c);

@@ -255,14 +255,20 @@ __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logi
 }
 
 // Rows of up to RT * NV float4s, a row per block held in registers, so each
-// row crosses HBM once: the row max and the sum of exp(x - max) (two block
+// row crosses HBM once: the row max and the sum of e = exp(x - max) (two block
 // reductions), lse and picked. With `dunit` set the block also writes, from
-// the registers, the gradient of the mean loss for an upstream gradient of
-// exactly 1: (exp(x - lse) - onehot) * (1 / n), what ce_bwd_k writes for
-// gloss = 1, so a backward seeded with 1 has nothing left to compute.
-// Measured at C3 (8192 x 32000): 512 x 16 runs the forward with the gradient
-// in 380 us (1024 x 8, held to one block per CU by its 68 VGPRs: 476 us;
-// 256 x 32: 417 us) and the forward alone in 181 us (streaming: 174 us).
+// the e it kept in the same registers, the gradient of the mean loss for an
+// upstream gradient of exactly 1, as the composed log_softmax VJP forms it
+// (functional.py:277-293 through ops.rs's exp/sum/log/sub VJPs):
+// gS * e with gS = (1 / n) * (1 / s), and gS * e - 1 / n at the target, so a
+// backward seeded with 1 has nothing left to compute. One exp per element:
+// with a second exp(x - lse) for the gradient the kernel spent about 39 VALU
+// instructions per element and ran at the VALU bound, not the HBM bound.
+// The zero-sum residue the reference routes to the argmax (the max VJP) is
+// rounding noise of the reference's own evaluation and is not formed.
+// Measured at C3 (8192 x 32000), two-exp form: 512 x 16 ran the forward with
+// the gradient in 380 us (1024 x 8, held to one block per CU by its 68 VGPRs:
+// 476 us; 256 x 32: 417 us) and the forward alone in 181 us (streaming: 174 us).
 template <int RT, int NV, bool GRAD, bool NTS>
 __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ logits,
                                                     const int64_t* __restrict__ targets, float* __restrict__ lse,
@@ -285,10 +291,13 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
   for (int k = 0; k < NV; ++k) m = fmaxf(m, max4(v[k]));
   m = group_max<RT>(m, lds);
   const float ms = m == NEG_INF ? 0.f : m;
+  // Lanes past the row hold -inf: their e is exp(-inf) = 0 and adds nothing.
   float s = 0.f;
 #pragma unroll
-  for (int k = 0; k < NV; ++k)
-    if (k * RT + t < c4) s += sum4(exp4(v[k] - ms));
+  for (int k = 0; k < NV; ++k) {
+    v[k] = exp4(v[k] - ms);
+    s += sum4(v[k]);
+  }
   s = group_sum<RT, float>(s, lds + RT / 64);
   int64_t tg = targets[row];
   if (tg < 0 || tg >= C) {
@@ -303,21 +312,25 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
   }
   if constexpr (GRAD) {
     const float scale = 1.0f / (float)n;
+    const float gs = scale * (1.0f / s);
+    // The target's float4 is slot kt of lane `own`; component jt.
+    const int ct = (int)(tg >> 2);
+    const int kt = ct / RT;
+    const bool own = ct - kt * RT == t;
+    const int jt = (int)(tg & 3);
     f4* q = reinterpret_cast<f4*>(dunit + row * C);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = k * RT + t;
       if (c < c4) {
-        f4 e = exp4(v[k] - l);
-        const int64_t base = (int64_t)c * 4;
-        if (tg >= base && tg < base + 4) {
-          const int j = (int)(tg - base);
-          if (j == 0) e.x -= 1.f;
-          else if (j == 1) e.y -= 1.f;
-          else if (j == 2) e.z -= 1.f;
-          else e.w -= 1.f;
+        f4 d = v[k] * gs;
+        if (k == kt && own) {
+          if (jt == 0) d.x -= scale;
+          else if (jt == 1) d.y -= scale;
+          else if (jt == 2) d.z -= scale;
+          else d.w -= scale;
         }
-        st_stream<NTS>(e * scale, q + c);
+        st_stream<NTS>(d, q + c);
       }
     }
   }

@@ -118,8 +118,11 @@ def test_cross_entropy_seeded_with_one_takes_the_forward_gradient(ox, F, c):
     """loss.backward() (the implicit seed 1) hands the logits the gradient
     the forward pass formed; an explicit seed, a loss used inside the graph,
     a retained second backward and rows whose class count is not a multiple
-    of 4 all run the backward kernel, with the same bits (twice the gradient when
-    doubled, which is exact in binary)."""
+    of 4 all run the backward kernel (twice its gradient, bit for bit, when
+    the loss is doubled; the retained pair adds the two). The one-pass and
+    the backward kernel's gradients agree within a few ulp; a class count
+    that is not a multiple of 4 takes the backward kernel both ways, bit for
+    bit."""
     say("cross_entropy backward seeds", c)
     r = np.random.default_rng(c)
     n = 16
@@ -140,9 +143,12 @@ def test_cross_entropy_seeded_with_one_takes_the_forward_gradient(ox, F, c):
         loss.backward(retain_graph=True)
         loss.backward()
     both = grad_of(twice)
-    assert np.array_equal(implicit.view(np.uint32), explicit.view(np.uint32))
-    assert np.array_equal((2 * implicit).view(np.uint32), doubled.view(np.uint32))
-    assert np.array_equal((2 * implicit).view(np.uint32), both.view(np.uint32))
+    if c % 4:
+        assert np.array_equal(implicit.view(np.uint32), explicit.view(np.uint32))
+    else:
+        assert np.allclose(implicit, explicit, rtol=1e-5, atol=1e-7 / n)
+    assert np.array_equal((2 * explicit).view(np.uint32), doubled.view(np.uint32))
+    assert np.array_equal((implicit + explicit).view(np.uint32), both.view(np.uint32))
     m = la.max(-1, keepdims=True)
     ls = la - m - np.log(np.exp(la - m).sum(-1, keepdims=True))
     want = (np.exp(ls) - np.eye(c, dtype=np.float32)[t]) / n

@@ -219,40 +219,49 @@ def _c3_inputs():
 
 
 def test_cross_entropy_c3_all_rows(hip):
+    """Both C3 paths on all 8192 rows: the one-pass forward that writes the
+    gradient (what backward() seeded with 1 takes) and the forward, then the
+    backward kernel from lse (any other upstream gradient)."""
     from oracle import closed_form, ref
-    say("cross_entropy C3 (8192, 32000): n*dlogits on all rows")
+    say("cross_entropy C3 (8192, 32000): n*dlogits on all rows, both paths")
     logits, t = _c3_inputs()
     n = logits.shape[0]
     dl, dt = D(hip, logits), D(hip, t)
     loss, lse = hip.cross_entropy_fwd(dl, dt)
     d = hip.cross_entropy_bwd(dl, dt, lse, D(hip, np.array([1.0], np.float32))).numpy()
-    parts, tot = [], 0.0
+    loss1, _, d1 = hip.cross_entropy_fwd_grad(dl, dt)
+    d1 = d1.numpy()
+    assert np.array_equal(loss1.numpy().view(np.uint32), loss.numpy().view(np.uint32))
+    parts, parts1, tot = [], [], 0.0
     for s in range(0, n, 512):
         sl = slice(s, s + 512)
         k = logits[sl].shape[0]
         # the oracle divides by its own row count: scale both to softmax - onehot
-        parts.append(assert_close_arb(d[sl] * n, ref.cross_entropy_bwd(logits[sl], t[sl]) * k,
-                                      closed_form.cross_entropy_grad(logits[sl], t[sl]) * k,
-                                      what=f"C3 n*dlogits rows {s}+"))
+        want = ref.cross_entropy_bwd(logits[sl], t[sl]) * k
+        exact = closed_form.cross_entropy_grad(logits[sl], t[sl]) * k
+        parts1.append(assert_close_arb(d1[sl] * n, want, exact, what=f"C3 one-pass n*dlogits rows {s}+"))
+        parts.append(assert_close_arb(d[sl] * n, want, exact, what=f"C3 n*dlogits rows {s}+"))
         ls = closed_form.log_softmax(logits[sl])
         tot += ls[np.arange(k), t[sl]].sum()
-    record("C3", "n*dlogits, all 8192 rows", _merge(parts))
+    record("C3", "n*dlogits, one pass, all 8192 rows", _merge(parts1))
+    record("C3", "n*dlogits, fwd then bwd, all 8192 rows", _merge(parts))
     l = float(loss.numpy()[0])
     err = abs(l - (-tot / n))
     assert err <= 1e-5 * abs(l)
     record("C3", "loss vs f64", {"n": 1, "worst_tol_f64": err / (1e-6 + 1e-5 * abs(tot / n)), "arbitrated": 0})
     # every row of softmax - onehot sums to zero
-    assert np.abs(d.astype(np.float64).sum(1) * n).max() < 1e-4
+    for g in (d, d1):
+        assert np.abs(g.astype(np.float64).sum(1) * n).max() < 1e-4
 
 
 def test_cross_entropy_c3_all_rows_through_F(hip, ox, F):
-    """F.cross_entropy(...).backward() runs the same kernels with the upstream
-    seed 1.0: its gradient equals the C-ABI's bit for bit on every row."""
+    """F.cross_entropy(...).backward() takes the one-pass kernel for the
+    implicit seed 1.0: its gradient equals oxi_cross_entropy_fwd_grad's bit
+    for bit on every row."""
     say("cross_entropy C3 via F.*: all rows equal the C-ABI path")
     logits, t = _c3_inputs()
     dl, dt = D(hip, logits), D(hip, t)
-    _, lse = hip.cross_entropy_fwd(dl, dt)
-    want = hip.cross_entropy_bwd(dl, dt, lse, D(hip, np.array([1.0], np.float32))).numpy()
+    want = hip.cross_entropy_fwd_grad(dl, dt)[2].numpy()
     L = ox.from_numpy(logits, True)
     F.cross_entropy(L, t.tolist()).backward()
     _same(L.grad.numpy(), want, "C3 dlogits via F.* vs C-ABI")
