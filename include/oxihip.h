@@ -310,7 +310,10 @@ int oxi_log_softmax_bwd(const float* y, const float* g, float* dx,
                         int64_t outer, int64_t len, int64_t inner);
 /* F.cross_entropy, mean reduction (functional.py:277-293), fused: writes the
  * scalar loss (1 float on device) and the per-row log-sum-exp `lse` (n floats).
- * `targets` are int64 class ids already resolved to [0, c). */
+ * `targets` are int64 class ids already resolved to [0, c). As the reference's
+ * sum(onehot * log_softmax(x)) does, a row whose non-target log-probability is
+ * -inf (a -inf logit, or x - max overflowing) makes the loss NaN (0 * -inf);
+ * lse and the gradient stay finite there. */
 int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets,
                           float* loss, float* lse, int64_t n, int64_t c);
 /* dlogits = (softmax(logits) - onehot(targets)) * gloss[0] / n. `gloss` is a

@@ -187,6 +187,30 @@ __device__ __forceinline__ float group_max(float v, float* lds) {
   return v;
 }
 
+// Two maxima over the group with one barrier (the _once contract above;
+// `lds` holds 2 * TPR/64 values).
+template <int TPR>
+__device__ __forceinline__ void group_max2_once(float& a, float& b, float* lds) {
+  a = wave_max(a);
+  b = wave_max(b);
+  if constexpr (TPR > 64) {
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    if (lane == 0) {
+      lds[wid] = a;
+      lds[TPR / 64 + wid] = b;
+    }
+    __syncthreads();
+    a = lds[0];
+    b = lds[TPR / 64];
+#pragma unroll
+    for (int i = 1; i < TPR / 64; ++i) {
+      a = fmaxf(a, lds[i]);
+      b = fmaxf(b, lds[TPR / 64 + i]);
+    }
+  }
+}
+
 template <int TPR>
 __device__ __forceinline__ float group_max_once(float v, float* lds) {
   v = wave_max(v);

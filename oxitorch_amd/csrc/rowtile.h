@@ -43,6 +43,7 @@ __device__ __forceinline__ void st_stream(T v, T* p) {
 constexpr float NEG_INF = -__builtin_huge_valf();
 
 __device__ __forceinline__ float max4(const f4& v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
+__device__ __forceinline__ float min4(const f4& v) { return fminf(fminf(v.x, v.y), fminf(v.z, v.w)); }
 __device__ __forceinline__ float sum4(const f4& v) { return (v.x + v.y) + (v.z + v.w); }
 __device__ __forceinline__ f4 exp4(const f4& v) { return f4{expf(v.x), expf(v.y), expf(v.z), expf(v.w)}; }
 

@@ -201,25 +201,48 @@ constexpr int CE_BS = 256;
 constexpr int CE_U = 4;   // forward: float4 loads in flight per thread per step
 constexpr int CE_BU = 1;  // backward: float4s per thread (one per thread streams fastest)
 
+// The reference picks the target's log-probability as
+// sum(onehot * log_softmax(x)) (functional.py:287-292): a non-target class
+// whose log-probability is -inf (x - max == -inf: a -inf logit, or one so far
+// below the max that the difference overflows) contributes 0 * -inf = NaN,
+// so that row's picked value, and the loss, is NaN. `mn` is the row's
+// minimum over its non-target logits; x - max is monotone in x.
+__device__ __forceinline__ bool onehot_nan(float mn, float m) { return mn - m == NEG_INF; }
+
+// v with component j replaced by +inf (out of a minimum).
+__device__ __forceinline__ f4 drop_lane(const f4& v, int j) {
+  const float P = -NEG_INF;
+  return f4{j == 0 ? P : v.x, j == 1 ? P : v.y, j == 2 ? P : v.z, j == 3 ? P : v.w};
+}
+
 // Rows longer than the register-row kernel takes (more than 16384 float4s,
 // or not vectorizable): one block per row, streaming it.
 // lse[row] = max + log(sum exp(x - max));
-// picked[row] = (x[t] - max) - log(sum)  (the reference's ls[row, t]).
+// picked[row] = (x[t] - max) - log(sum)  (the reference's ls[row, t]), or
+// NaN where the reference's one-hot product makes it NaN (onehot_nan).
 __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logits, const int64_t* __restrict__ targets,
                                                   float* __restrict__ lse, float* __restrict__ picked, int64_t n, int C,
                                                   int vec, int* __restrict__ guard) {
   __shared__ float lds[2 * (CE_BS / 64)];
   const int64_t row = blockIdx.x;
   const float* xr = logits + row * C;
+  int64_t tg = targets[row];
+  const bool bad = tg < 0 || tg >= C;
+  if (bad) tg = 0;
+  float mn = -NEG_INF;
   Online o;
   if (vec) {
     const f4* p = reinterpret_cast<const f4*>(xr);
     const int c4 = C >> 2;
+    const int ct = (int)(tg >> 2);
+    const int jt = (int)(tg & 3);
     int c = threadIdx.x;
     for (; c + (CE_U - 1) * CE_BS < c4; c += CE_U * CE_BS) {
       f4 v[CE_U];
 #pragma unroll
       for (int u = 0; u < CE_U; ++u) v[u] = ld_stream(p + c + u * CE_BS);
+#pragma unroll
+      for (int u = 0; u < CE_U; ++u) mn = fminf(mn, min4(c + u * CE_BS == ct ? drop_lane(v[u], jt) : v[u]));
       float cm = max4(v[0]);
 #pragma unroll
       for (int u = 1; u < CE_U; ++u) cm = fmaxf(cm, max4(v[u]));
@@ -237,26 +260,32 @@ __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logi
         for (int u = 0; u < CE_U; ++u) o.add4(v[u]);
       }
     }
-    for (; c < c4; c += CE_BS) o.add4(p[c]);
+    for (; c < c4; c += CE_BS) {
+      const f4 v = p[c];
+      o.add4(v);
+      mn = fminf(mn, min4(c == ct ? drop_lane(v, jt) : v));
+    }
   } else {
-    for (int c = threadIdx.x; c < C; c += CE_BS) o.add1(xr[c]);
+    for (int c = threadIdx.x; c < C; c += CE_BS) {
+      const float v = xr[c];
+      o.add1(v);
+      if (c != tg) mn = fminf(mn, v);
+    }
   }
   group_online<CE_BS>(o, lds);
+  mn = -group_max<CE_BS>(-mn, lds);
   if (threadIdx.x == 0) {
-    int64_t t = targets[row];
-    if (t < 0 || t >= C) {
-      atomicOr(guard, 1);
-      t = 0;
-    }
+    if (bad) atomicOr(guard, 1);
     const float L = logf(o.s);
     lse[row] = o.m + L;
-    picked[row] = (xr[t] - o.m) - L;
+    picked[row] = onehot_nan(mn, o.m) ? __builtin_nanf("") : (xr[tg] - o.m) - L;
   }
 }
 
 // Rows of up to RT * NV float4s, a row per block held in registers, so each
-// row crosses HBM once: the row max and the sum of e = exp(x - max) (two block
-// reductions), lse and picked. With `dunit` set the block also writes, from
+// row crosses HBM once: the row max (with the non-target minimum that
+// onehot_nan needs, in the same reduction) and the sum of e = exp(x - max)
+// (two block reductions), lse and picked. With `dunit` set the block also writes, from
 // the e it kept in the same registers, the gradient of the mean loss for an
 // upstream gradient of exactly 1, as the composed log_softmax VJP forms it
 // (functional.py:277-293 through ops.rs's exp/sum/log/sub VJPs):
@@ -274,7 +303,8 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
                                                     const int64_t* __restrict__ targets, float* __restrict__ lse,
                                                     float* __restrict__ picked, float* __restrict__ dunit, int64_t n,
                                                     int C, int* __restrict__ guard) {
-  __shared__ float lds[2 * (RT / 64)];
+  // slot sets: the max and the non-target minimum, then the sum
+  __shared__ float lds[3 * (RT / 64)];
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x;
   const int c4 = C >> 2;
@@ -286,10 +316,23 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
     const int c = k * RT + t;
     v[k] = c < c4 ? ld_stream(p + c) : f4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
   }
+  int64_t tg = targets[row];
+  const bool bad = tg < 0 || tg >= C;
+  if (bad) tg = 0;
+  // The target's float4 is slot kt of lane `own`; component jt.
+  const int ct = (int)(tg >> 2);
+  const int kt = ct / RT;
+  const bool own = ct - kt * RT == t;
+  const int jt = (int)(tg & 3);
   float m = NEG_INF;
+  float mn = -NEG_INF;  // minimum over the non-target logits (onehot_nan)
 #pragma unroll
-  for (int k = 0; k < NV; ++k) m = fmaxf(m, max4(v[k]));
-  m = group_max<RT>(m, lds);
+  for (int k = 0; k < NV; ++k) {
+    m = fmaxf(m, max4(v[k]));
+    if (k * RT + t < c4) mn = fminf(mn, min4(k == kt && own ? drop_lane(v[k], jt) : v[k]));
+  }
+  float nmn = -mn;
+  group_max2_once<RT>(m, nmn, lds);
   const float ms = m == NEG_INF ? 0.f : m;
   // Lanes past the row hold -inf: their e is exp(-inf) = 0 and adds nothing.
   float s = 0.f;
@@ -298,26 +341,16 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
     v[k] = exp4(v[k] - ms);
     s += sum4(v[k]);
   }
-  s = group_sum<RT, float>(s, lds + RT / 64);
-  int64_t tg = targets[row];
-  if (tg < 0 || tg >= C) {
-    if (t == 0) atomicOr(guard, 1);
-    tg = 0;
-  }
+  s = group_sum_once<RT, float>(s, lds + 2 * (RT / 64));
   const float L = logf(s);
-  const float l = m + L;
   if (t == 0) {
-    lse[row] = l;
-    picked[row] = (xr[tg] - m) - L;
+    if (bad) atomicOr(guard, 1);
+    lse[row] = m + L;
+    picked[row] = onehot_nan(-nmn, m) ? __builtin_nanf("") : (xr[tg] - m) - L;
   }
   if constexpr (GRAD) {
     const float scale = 1.0f / (float)n;
     const float gs = scale * (1.0f / s);
-    // The target's float4 is slot kt of lane `own`; component jt.
-    const int ct = (int)(tg >> 2);
-    const int kt = ct / RT;
-    const bool own = ct - kt * RT == t;
-    const int jt = (int)(tg & 3);
     f4* q = reinterpret_cast<f4*>(dunit + row * C);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {

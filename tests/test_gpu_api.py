@@ -155,6 +155,28 @@ def test_cross_entropy_seeded_with_one_takes_the_forward_gradient(ox, F, c):
     assert np.allclose(implicit, want, rtol=1e-4, atol=1e-6)
 
 
+@pytest.mark.parametrize("c", [1000, 1003])
+def test_cross_entropy_masked_logits(ox, F, c):
+    """A -inf logit at a non-target class: the loss is NaN, as the
+    reference's sum(onehot * log_softmax) makes it, and backward() still gives
+    the finite gradient (0 at the masked class), through the one-pass kernel
+    (c = 1000) and the two calls (c = 1003)."""
+    from oracle import ref
+    say("cross_entropy masked logits via F.*", c)
+    r = np.random.default_rng(c)
+    la = (r.standard_normal((8, c), dtype=np.float32) * 2).astype(np.float32)
+    t = r.integers(0, c, 8)
+    la[3, (t[3] + 1) % c] = -np.inf
+    x = _t(ox, la, True)
+    loss = F.cross_entropy(x, t)
+    assert np.isnan(loss.item())
+    loss.backward()
+    g = x.grad.numpy()
+    want = ref.cross_entropy_bwd(la, t)
+    assert np.isfinite(g).all() and g[3, (t[3] + 1) % c] == 0.0
+    assert np.allclose(8 * g, 8 * want, rtol=1e-5, atol=1e-5)
+
+
 def test_cross_entropy_rejects_wrong_batch(ox, F):
     with pytest.raises(ValueError, match="targets"):
         F.cross_entropy(_t(ox, np.zeros((2, 3))), [0, 1, 2])

@@ -280,6 +280,70 @@ def test_cross_entropy_fwd_grad_is_fwd_then_bwd(hip, n, c):
         assert_close_arb(arr.numpy()[rows] * n, want, exact, what=f"({n}, {c}) n*dlogits, {what}")
 
 
+def _ce_special_batches(c):
+    """Two-row batches, row 0 plain, row 1 special: (name, logits, targets)."""
+    r = rng(c)
+    out = []
+    for name in ("masked logit", "masked target", "overflowing gap", "overflowing target", "all -inf", "+inf",
+                 "nan"):
+        x = (r.standard_normal((2, c), dtype=np.float32) * 2).astype(np.float32)
+        t = np.array([3, 7], np.int64)
+        row = x[1]
+        if name == "masked logit":
+            row[[0, c // 2, c - 1]] = -np.inf
+        elif name == "masked target":
+            row[7] = -np.inf
+        elif name == "overflowing gap":  # x - max overflows to -inf on a non-target class
+            row[5], row[c - 2] = 3e38, -3e38
+        elif name == "overflowing target":
+            row[5], row[7] = 3e38, -3e38
+        elif name == "all -inf":
+            row[:] = -np.inf
+        elif name == "+inf":
+            row[c // 3] = np.inf
+        else:
+            row[c // 3] = np.nan
+        out.append((name, x, t))
+    return out
+
+
+@pytest.mark.parametrize("c", [1000, 1003, 65540])
+def test_cross_entropy_special_values(hip, c):
+    """Rows with -inf, overflowing, +inf and NaN logits give the reference's
+    values: its picked log-probability is sum(onehot * log_softmax(x))
+    (functional.py:287-292), so a non-target log-probability of -inf makes
+    the loss NaN (0 * -inf) while the gradient stays finite; a -inf target
+    gives an infinite loss; +inf, NaN and all -inf rows are NaN throughout.
+    Register rows (c = 1000, with the one-pass gradient), the streaming
+    kernel (1003, and 65540 float4 rows), the backward from lse."""
+    from oracle import ref
+    for name, x, t in _ce_special_batches(c):
+        say("cross_entropy special values", c, name)
+        dx, dt = D(hip, x), D(hip, t)
+        loss, lse = hip.cross_entropy_fwd(dx, dt)
+        paths = [("fwd then bwd", float(loss.numpy()[0]),
+                  hip.cross_entropy_bwd(dx, dt, lse, D(hip, np.ones(1, np.float32))).numpy())]
+        if c % 4 == 0 and c <= 65536:
+            l1, _, d1 = hip.cross_entropy_fwd_grad(dx, dt)
+            paths.append(("one pass", float(l1.numpy()[0]), d1.numpy()))
+        want_l = ref.cross_entropy_fwd(x, t)
+        want_d = ref.cross_entropy_bwd(x, t)
+        for what, l, d in paths:
+            tag = f"c={c} {name} {what}"
+            if np.isnan(want_l):
+                assert np.isnan(l), f"{tag}: loss {l}, reference NaN"
+            elif np.isinf(want_l):
+                assert l == want_l, f"{tag}: loss {l}, reference {want_l}"
+            else:
+                assert abs(l - want_l) <= 1e-5 * abs(want_l) + 1e-6, f"{tag}: loss {l} vs {want_l}"
+            assert np.array_equal(np.isnan(d), np.isnan(want_d)), f"{tag}: NaN placement differs"
+            assert np.array_equal(np.isinf(d), np.isinf(want_d)), f"{tag}: inf placement differs"
+            ok = np.isfinite(want_d)
+            # the reference adds its zero-sum residue at the argmax: compare elementwise within
+            # the reference path's tolerance, n * dlogits being O(1)
+            assert np.allclose(2 * d[ok], 2 * want_d[ok], rtol=1e-5, atol=1e-5), f"{tag}: dlogits differ"
+
+
 def test_cross_entropy_fwd_grad_refusals(hip):
     """Rows past 65536 classes or of a class count that is not a multiple of
     4 are refused before any launch (the two-call path serves them)."""

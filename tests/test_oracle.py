@@ -121,6 +121,30 @@ def test_kat_cross_entropy():
     assert np.allclose(g, want, rtol=1e-4, atol=1e-6)
 
 
+def test_cross_entropy_masked_logits_follow_the_onehot_product():
+    """The reference picks ls[i, t] as sum(onehot * ls) (functional.py:287-292):
+    a -inf logit at a non-target class gives 0 * -inf = NaN in that sum, so
+    the loss is NaN, while a -inf target alone gives +inf; the gradient's
+    onehot factor stays finite either way (it is g * onehot). An oracle that
+    read ls[i, t] directly would give a finite loss for the first case."""
+    lg = np.array([[1.0, 2.0, 3.0, 0.5], [3.0, 1.0, 2.0, 0.0]], np.float32)
+    t = [2, 0]
+    base = ref.cross_entropy_fwd(lg, t)
+    assert np.isfinite(base)
+    masked = lg.copy()
+    masked[1, 3] = -np.inf
+    assert np.isnan(ref.cross_entropy_fwd(masked, t))
+    g = ref.cross_entropy_bwd(masked, t)
+    assert np.isfinite(g).all() and g[1, 3] == 0.0
+    masked_t = lg.copy()
+    masked_t[1, 0] = -np.inf
+    assert ref.cross_entropy_fwd(masked_t, t) == np.inf
+    # x - max overflowing to -inf acts as a -inf logit
+    far = lg.copy()
+    far[1, 2], far[1, 3] = 3e38, -3e38
+    assert np.isnan(ref.cross_entropy_fwd(far, t))
+
+
 def test_kat_reductions():
     """crates/oxi-tensor/src/ops.rs:370-381, tests.rs:180-196, python/tests/test_smoke.py:107-121."""
     d = np.array([[1.0, 2.0, 3.0, 4.0]], np.float32)
