@@ -299,3 +299,46 @@ def test_lead_sum_matches_node_by_node(hip, kind, act):
         for part in ("dw", "db"):
             if part in gots:
                 same_specials(gots[part].numpy(), wants[part].numpy(), f"{tag} {part}")
+
+
+@pytest.mark.parametrize("opt", ["sgd", "sgd_nesterov", "adamw", "adam"])
+def test_optimizer_steps(hip, opt):
+    """Two optimizer steps over every pairing of special parameter value and
+    special gradient (the state then holds specials too): parameters and
+    state as the oracle's steps leave them."""
+    from oracle import ref
+    say("special values", opt)
+    p0 = np.repeat(REGISTRY_X, len(REGISTRY_X))
+    g = np.tile(REGISTRY_X, len(REGISTRY_X))
+    p, st1, st2 = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+    dp, dg, d1, d2 = D(hip, p0), D(hip, g), D(hip, st1), D(hip, st2)
+    for t in (1, 2):
+        if opt.startswith("sgd"):
+            nest = opt == "sgd_nesterov"
+            p = ref.sgd_step(p, g, st1, 0.1, momentum=0.9, nesterov=nest)
+            dp = hip.sgd_step(dp, dg, d1, 0.1, momentum=0.9, nesterov=nest)
+        else:
+            dec = opt == "adamw"
+            p = ref.adamw_step(p, g, st1, st2, t, 1e-3, weight_decay=0.01, decoupled=dec)
+            dp = hip.adamw_step(dp, dg, d1, d2, t, 1e-3, weight_decay=0.01, decoupled=dec)
+        same_specials(dp.numpy(), p, f"{opt} step {t} parameters")
+        same_specials(d1.numpy(), st1, f"{opt} step {t} first state")
+        if not opt.startswith("sgd"):
+            same_specials(d2.numpy(), st2, f"{opt} step {t} second state")
+
+
+def test_embedding_vjp_sums(hip):
+    """Gradient rows holding NaN and +-inf summed into shared ids (and ids
+    seen once): the table's rows as the oracle's position-order sums."""
+    from oracle import ref
+    say("special values embedding VJP")
+    r = rng(31)
+    V, H = 64, 96
+    ids = np.array([3, 5, 3, 7, 3, 9, 5, 11, 3, 3, 12, 13] * 4, np.int64)
+    g = r.standard_normal((len(ids), H), dtype=np.float32)
+    g[0, 4], g[2, 4] = INF, -INF      # +inf + -inf in id 3: NaN
+    g[1, 7] = NAN                     # NaN in id 5
+    g[3, 9], g[15, 9] = INF, INF      # +inf twice in id 7
+    g[5, :] = 3e38                    # one row, id 9, four times: overflows
+    gw = hip.embedding_bwd(D(hip, g), hip.DeviceArray.from_numpy(ids), V).numpy()
+    same_specials(gw, ref.index_select_bwd(g, (V, H), 0, ids), "embedding VJP")
