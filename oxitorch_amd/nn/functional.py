@@ -118,9 +118,12 @@ def mse_loss(pred, target):
 def cross_entropy(logits, targets):
     """Mean cross-entropy; `targets` is a flat list of int class indices.
 
-    Fused: one streaming pass forward (per-row log-sum-exp and the picked
-    log-probability), one backward writing (softmax - onehot) * g / n. The
-    argument checks mirror the reference's: a batch-size mismatch raises
+    Fused: the forward reads each row once (its log-sum-exp and picked
+    log-probability, NaN where the reference's sum(onehot * log_softmax)
+    is); when the logits require grad it also writes the gradient that
+    backward() with its implicit seed of 1 hands them, and any other
+    upstream gradient g runs one backward pass writing
+    (softmax - onehot) * g / n. The argument checks mirror the reference's: a batch-size mismatch raises
     ValueError mentioning the targets, and class ids follow numpy indexing
     (negatives wrap, out-of-range raises IndexError)."""
     n, classes = logits.shape
