@@ -692,6 +692,9 @@ struct SortPlan {
   hipEvent_t ready = nullptr;   // recorded on the side stream after the sort
   mutable int applies = 0;  // a second apply (retain_graph) re-zeroes the owner count
   bool recorded = false;    // `ready` holds the sort's completion
+  // the library stream is already ordered after the sort (an apply waited
+  // for `ready`, or saw it complete): freeing the plan needs no wait
+  mutable bool ordered = false;
 };
 
 int build_plan(const int64_t* idx, int64_t n, int64_t len, hipStream_t s, SortPlan* p) {
@@ -930,9 +933,12 @@ int oxi_index_select_bwd_apply(const void* plan, const float* g, int64_t outer, 
   OXI_CHECK_INIT();
   // a cross-stream wait costs a barrier packet on the library stream: skip it
   // when the sort has already finished
-  if (p.recorded && hipEventQuery(p.ready) != hipSuccess) {
-    hipError_t e = hipStreamWaitEvent(stream(), p.ready, 0);
-    if (e != hipSuccess) return fail_hip(e, "index_select_bwd_apply: waiting for the plan");
+  if (p.recorded && !p.ordered) {
+    if (hipEventQuery(p.ready) != hipSuccess) {
+      hipError_t e = hipStreamWaitEvent(stream(), p.ready, 0);
+      if (e != hipSuccess) return fail_hip(e, "index_select_bwd_apply: waiting for the plan");
+    }
+    p.ordered = true;
   }
   return apply_plan(p, g, outer, inner, grad);
 }
@@ -941,8 +947,10 @@ int oxi_index_select_bwd_plan_free(void* plan) {
   if (!plan) return OXI_OK;
   SortPlan* p = static_cast<SortPlan*>(plan);
   // the library stream passes the plan's sort before its memory can be
-  // reused, and before its events go back to the pool
-  if (p->recorded && ensure_init() && hipEventQuery(p->ready) != hipSuccess)
+  // reused, and before its events go back to the pool (already so after an
+  // apply; the next plan's sort waits for the library stream's work queued
+  // before it, this plan's apply included, so it cannot reuse the memory early)
+  if (p->recorded && !p->ordered && ensure_init() && hipEventQuery(p->ready) != hipSuccess)
     (void)hipStreamWaitEvent(stream(), p->ready, 0);
   // a plan whose build failed part-way has no completion event: kernels it
   // queued may still run on the side stream, so drain it (error path only)
