@@ -137,5 +137,19 @@ def cross_entropy(logits, targets):
     return _native.cross_entropy(logits, t)
 
 
-def linear(*args, **kwargs):
-    raise NotImplementedError("linear (SGEMM) is outside this build's device hot path")
+def _outside(what):
+    def op(*args, **kwargs):
+        raise NotImplementedError(f"{what} is outside this build's device hot path")
+    op.__name__ = what.split(" ")[0]
+    op.__doc__ = f"The reference's {what}: not part of this build; raises NotImplementedError."
+    return op
+
+
+# The reference's GEMM, convolution, pooling and dropout entry points
+# (functional.py:23-47,49-55,104-148,150-181,255-268) are outside the device
+# hot path; calling one says so instead of failing on a missing name.
+linear = _outside("linear (SGEMM)")
+bmm = _outside("bmm (batched GEMM)")
+conv2d = _outside("conv2d (im2col + GEMM)")
+max_pool2d = _outside("max_pool2d")
+dropout = _outside("dropout")

@@ -80,6 +80,24 @@ def Sigmoid():
     return _Activation(F.sigmoid)
 
 
+def LeakyReLU(negative_slope=0.01):
+    return _Activation(lambda x: F.leaky_relu(x, negative_slope))
+
+
+def _outside_layer(name, what):
+    def layer(*args, **kwargs):
+        raise NotImplementedError(f"nn.{name} ({what}) is outside this build's device hot path")
+    layer.__name__ = name
+    return layer
+
+
+# layers.py:20-92,134-164 of the reference: not part of this build
+Linear = _outside_layer("Linear", "SGEMM")
+Conv2d = _outside_layer("Conv2d", "im2col + GEMM")
+MaxPool2d = _outside_layer("MaxPool2d", "window gather + max")
+Dropout = _outside_layer("Dropout", "host RNG masks")
+
+
 class Softmax(Module):
     """F.softmax along `dim`."""
 

@@ -68,6 +68,10 @@ def test_activations_values(ox, F):
     assert np.allclose(F.silu(x).numpy(), r / (1 + np.exp(-r)), atol=1e-6)
     c = np.sqrt(2 / np.pi)
     assert np.allclose(F.gelu(x).numpy(), 0.5 * r * (1 + np.tanh(c * (r + 0.044715 * r ** 3))), atol=1e-5)
+    # layers.py:183-188: LeakyReLU is F.leaky_relu
+    import oxitorch_amd.nn as nn
+    assert np.allclose(F.leaky_relu(x, 0.2).numpy(), np.where(r > 0, r, 0.2 * r), atol=1e-7)
+    assert np.array_equal(nn.LeakyReLU(0.2)(x).numpy(), F.leaky_relu(x, 0.2).numpy())
 
 
 def test_layer_norm_value_and_grads(ox, F):

@@ -425,3 +425,20 @@ def test_loader_argument_checks(ox):
 
     with pytest.raises(ValueError, match="batch_size must be >= 1"):
         DataLoader(TensorDataset(cpu(ox, np.zeros((3, 2)))), batch_size=0)
+
+
+def test_out_of_scope_names_raise_not_implemented():
+    """The reference's GEMM, convolution, pooling and dropout names
+    (nn/functional.py:23-55,104-181,255-268, nn/layers.py:20-92,134-164)
+    exist and say they are outside this build when called."""
+    import oxitorch_amd.nn as nn
+    import oxitorch_amd.nn.functional as F
+
+    for fn in (F.linear, F.bmm, F.conv2d, F.max_pool2d, F.dropout, nn.linear, nn.bmm, nn.conv2d, nn.max_pool2d,
+               nn.dropout):
+        with pytest.raises(NotImplementedError, match="outside this build's device hot path"):
+            fn(None)
+    for layer in (nn.Linear, nn.Conv2d, nn.MaxPool2d, nn.Dropout):
+        with pytest.raises(NotImplementedError, match="outside this build's device hot path"):
+            layer(4, 4)
+    assert callable(nn.LeakyReLU)
