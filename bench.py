@@ -30,7 +30,12 @@ those fusions (the host core with OXI_FUSE_NORM_ACT=0, or C3 with another
 seed).
 
 Time per step comes from HIP events recorded on the library stream (the
-stream every liboxihip kernel runs on) around K back-to-back steps.
+stream every liboxihip kernel runs on) around K back-to-back steps, after W
+untimed warmup steps. Each config takes that timing last, after its other
+measurements below, so the device has been running the workload (as in a
+training loop) rather than idling through the host's set-up of it; Python's
+cycle collector is off around the timed loops of C-ABI calls (as in timeit),
+so that no collection pass lands among them.
 
 Per config:
 - kernels: each C-ABI call of the step timed alone over back-to-back
@@ -56,6 +61,7 @@ Prints ONE JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import re
@@ -740,19 +746,37 @@ WORKLOADS = {"c1": C1, "c2": C2, "c3": C3, "c4": C4, "c5": C5, "f2": F2, "f3": F
 
 # ---------------------------------------------------------------------------
 
+class _NoGC:
+    """Python's cycle collector off around a timed loop of C-ABI calls (as
+    timeit does): a collection pass started by the objects earlier
+    measurements left would otherwise land in a few hundred microseconds of
+    timed launches. The F.* step is timed with the collector on, as a user
+    runs it."""
+
+    def __enter__(self):
+        gc.collect()
+        self.was = gc.isenabled()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        if self.was:
+            gc.enable()
+
+
 def time_steps(hip, kernels, steps, host=None):
     """Device time per step over `steps` back-to-back steps (HIP events on the
     library stream); `host`, when given, receives the host's issue time per
     step (a host that issues slower than the device runs leaves the device idle)."""
     t = hip.Timer()
     hip.sync()
-    t.start()
-    h0 = time.perf_counter()
-    for _ in range(steps):
-        for _, fn, _ in kernels:
-            fn()
-    h1 = time.perf_counter()
-    ms = t.stop()
+    with _NoGC():
+        t.start()
+        h0 = time.perf_counter()
+        for _ in range(steps):
+            for _, fn, _ in kernels:
+                fn()
+        h1 = time.perf_counter()
+        ms = t.stop()
     hip.sync()
     if host is not None:
         host.append((h1 - h0) * 1e3 / steps)
@@ -771,10 +795,11 @@ def time_calls(hip, kernels, reps):
         fn()
         fn()
         hip.sync()
-        t.start()
-        for _ in range(reps):
-            fn()
-        avg = t.stop() / reps
+        with _NoGC():
+            t.start()
+            for _ in range(reps):
+                fn()
+            avg = t.stop() / reps
         out[label] = {"ms": avg, "bytes": nbytes, "gbs": nbytes / (avg * 1e-3) / 1e9 if nbytes else None}
     hip.sync()
     return out
@@ -965,7 +990,13 @@ def time_dropin(hip, wl, steps, warmup, hbm):
 
 
 def run_config(hip, key, args):
-    """Everything measured for one config; returns its block of the line."""
+    """Everything measured for one config; returns its block of the line.
+
+    The step's own timing (W untimed warmup steps, then exactly K timed
+    steps) comes last, after the per-call, node-by-node, same-bytes, cold-cache
+    and F.* measurements: by then the device has run the workload for a while,
+    as it has in a training loop, rather than idling through the host's
+    set-up of the workload just before."""
     log(f"[{key}] building workload")
     wl = WORKLOADS[key](hip)
     kernels = wl.kernels()
@@ -973,33 +1004,12 @@ def run_config(hip, key, args):
         for _, fn, _ in kernels:
             fn()
     hip.sync()
-    log(f"[{key}] timing {args.steps} steps")
-    host_ms = []
-    ms = time_steps(hip, kernels, args.steps, host_ms)
     reps = max(5, min(args.steps, 20))
+    log(f"[{key}] timing each C-ABI call")
     per = time_calls(hip, kernels, reps)
     hbm = sum(b for _, _, b in kernels)
-    gbs = hbm / (ms * 1e-3) / 1e9
-    per_op = wl.bytes_per_step / (ms * 1e-3) / 1e9
     traffic = pmc_traffic(key)
-    block = {
-        "workload": wl.name,
-        "ms_per_step": round(ms, 5),
-        "gbs": round(gbs, 2),
-        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
-        "rows_per_step": wl.rows,
-        "rows_per_s": round(wl.rows / (ms * 1e-3), 1),
-        "hbm_bytes_per_step": hbm,
-        "launched": "the host core's default launch sequence (graph fusions on)",
-        "per_op_bytes_per_step": wl.bytes_per_step,
-        "per_op_gbs": round(per_op, 2),
-        "per_op_pct_of_peak": round(100.0 * per_op / PEAK_HBM_GBS, 2),
-        "host_issue_ms_per_step": round(host_ms[0], 5),
-        "kernels": _calls_json(per),
-        "roofline": roofline(per, traffic, f"profiles/pmc_traffic_{key}.md"),
-    }
-    if isinstance(wl, C4):
-        block["distinct_ids"] = wl.unique_rows  # the rows of W the gather's HBM bytes count
+    block = {}
     if hasattr(wl, "unfused_kernels"):
         uk = wl.unfused_kernels()
         for _ in range(max(args.warmup, 1)):
@@ -1033,10 +1043,39 @@ def run_config(hip, key, args):
                                         "gbs": round(wl.bytes_per_step / (ms_alt * 1e-3) / 1e9, 2)}
     if hasattr(wl, "dropin") and not args.no_dropin:
         log(f"[{key}] timing the F.*/backward() step")
-        d = time_dropin(hip, wl, max(3, min(args.steps, 10)), args.warmup, hbm)
+        block["dropin"] = time_dropin(hip, wl, max(3, min(args.steps, 10)), args.warmup, hbm)
+    for _ in range(args.warmup):
+        for _, fn, _ in kernels:
+            fn()
+    hip.sync()
+    log(f"[{key}] timing {args.steps} steps")
+    host_ms = []
+    ms = time_steps(hip, kernels, args.steps, host_ms)
+    gbs = hbm / (ms * 1e-3) / 1e9
+    per_op = wl.bytes_per_step / (ms * 1e-3) / 1e9
+    head = {
+        "workload": wl.name,
+        "ms_per_step": round(ms, 5),
+        "gbs": round(gbs, 2),
+        "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "rows_per_step": wl.rows,
+        "rows_per_s": round(wl.rows / (ms * 1e-3), 1),
+        "hbm_bytes_per_step": hbm,
+        "launched": "the host core's default launch sequence (graph fusions on)",
+        "per_op_bytes_per_step": wl.bytes_per_step,
+        "per_op_gbs": round(per_op, 2),
+        "per_op_pct_of_peak": round(100.0 * per_op / PEAK_HBM_GBS, 2),
+        "host_issue_ms_per_step": round(host_ms[0], 5),
+        "kernels": _calls_json(per),
+        "roofline": roofline(per, traffic, f"profiles/pmc_traffic_{key}.md"),
+    }
+    if isinstance(wl, C4):
+        head["distinct_ids"] = wl.unique_rows  # the rows of W the gather's HBM bytes count
+    block = {**head, **block}
+    if "dropin" in block:
+        d = block["dropin"]
         d["vs_capi_ms_per_step"] = block["ms_per_step"]
         d["overhead_pct"] = round(100.0 * (d["ms_per_step"] / block["ms_per_step"] - 1.0), 1)
-        block["dropin"] = d
     block["cpu_baseline"] = None
     if not args.no_cpu and args.cpu_seconds > 0:
         log(f"[{key}] timing the CPU oracle baseline")
