@@ -31,11 +31,9 @@ seed).
 
 Time per step comes from HIP events recorded on the library stream (the
 stream every liboxihip kernel runs on) around K back-to-back steps, after W
-untimed warmup steps. Each config takes that timing last, after its other
-measurements below, so the device has been running the workload (as in a
-training loop) rather than idling through the host's set-up of it; Python's
-cycle collector is off around the timed loops of C-ABI calls (as in timeit),
-so that no collection pass lands among them.
+untimed warmup steps, taken last among a config's measurements below.
+Python's cycle collector is off around the timed loops of C-ABI calls (as in
+timeit), so that no collection pass lands among them.
 
 Per config:
 - kernels: each C-ABI call of the step timed alone over back-to-back
@@ -994,9 +992,7 @@ def run_config(hip, key, args):
 
     The step's own timing (W untimed warmup steps, then exactly K timed
     steps) comes last, after the per-call, node-by-node, same-bytes, cold-cache
-    and F.* measurements: by then the device has run the workload for a while,
-    as it has in a training loop, rather than idling through the host's
-    set-up of the workload just before."""
+    and F.* measurements."""
     log(f"[{key}] building workload")
     wl = WORKLOADS[key](hip)
     kernels = wl.kernels()
