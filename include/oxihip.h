@@ -313,7 +313,8 @@ int oxi_log_softmax_bwd(const float* y, const float* g, float* dx,
  * `targets` are int64 class ids already resolved to [0, c). As the reference's
  * sum(onehot * log_softmax(x)) does, a row whose non-target log-probability is
  * -inf (a -inf logit, or x - max overflowing) makes the loss NaN (0 * -inf);
- * lse and the gradient stay finite there. */
+ * lse and the gradient stay finite there. n == 0 writes a loss of -0.0 (the
+ * reference's mean of no rows is 0, bindings lib.rs:126-143, negated). */
 int oxi_cross_entropy_fwd(const float* logits, const int64_t* targets,
                           float* loss, float* lse, int64_t n, int64_t c);
 /* dlogits = (softmax(logits) - onehot(targets)) * gloss[0] / n. `gloss` is a

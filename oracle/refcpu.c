@@ -345,7 +345,10 @@ EXPORT void ref_cross_entropy_fwd(const float* logits, const int64_t* targets, f
     for (int64_t k = 0; k < c; ++k) picked += (k == targets[r] ? 1.0f : 0.0f) * ls[k];
     psum += picked;
   }
-  const float mean = psum / (float)n; /* reduce_all Mean over dim 0 (bindings lib.rs:126-137) */
+  /* picked.mean(): reduce_all (bindings lib.rs:126-143) reduces with
+   * reduce_strip, whose Mean of an empty strip is 0 (ops.rs:247-249), so an
+   * empty batch gives -(0.0) = -0.0 */
+  const float mean = n > 0 ? psum / (float)n : 0.0f;
   *loss = -mean;
   free(ls);
 }

@@ -574,7 +574,9 @@ int ce_forward(const char* what, const float* logits, const int64_t* targets, fl
   if (c > ((int64_t)1 << 30) || n > ((int64_t)1 << 31) - 1)
     return fail(OXI_INVALID_ARGUMENT, "%s: size exceeds the kernel limits", what);
   OXI_CHECK_INIT();
-  if (n == 0) return oxi_fill(loss, 1, __builtin_nanf(""));  // mean of nothing (Tensor::mean_all, lib.rs:589-593)
+  // picked.mean() of no rows: reduce_all's Mean of an empty strip is 0
+  // (bindings lib.rs:126-143, ops.rs:247-249), and the loss is its negation
+  if (n == 0) return oxi_fill(loss, 1, -0.0f);
   if (c == 0) return fail(OXI_INVALID_ARGUMENT, "%s: zero classes", what);
   if (!logits || !targets || !lse) return fail(OXI_INVALID_ARGUMENT, "%s: NULL tensor pointer", what);
   const int vec = (c % 4 == 0 && aligned16({logits})) ? 1 : 0;

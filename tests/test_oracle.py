@@ -593,3 +593,11 @@ def test_masked_select_drops_nan_values():
     x = np.array([1.0, np.nan, 3.0], np.float32)
     m = np.ones(3, np.float32)
     assert ref.masked_select(x, m).tolist() == [1.0, 3.0]
+
+
+def test_cross_entropy_of_an_empty_batch_is_negative_zero():
+    """picked.mean() over no rows goes through reduce_all, whose Mean of an
+    empty strip is 0 (bindings lib.rs:126-143, ops.rs:247-249), so the loss
+    is -(0.0) = -0.0, not the 0/0 of Tensor::mean_all."""
+    loss = ref.cross_entropy_fwd(np.zeros((0, 5), np.float32), np.zeros(0, np.int64))
+    assert loss == 0.0 and np.signbit(loss)
