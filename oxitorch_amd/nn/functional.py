@@ -127,7 +127,14 @@ def cross_entropy(logits, targets):
     ValueError mentioning the targets, and class ids follow numpy indexing
     (negatives wrap, out-of-range raises IndexError)."""
     n, classes = logits.shape
-    t = np.asarray(targets, dtype=np.int64).ravel()
+    t = np.asarray(targets)
+    if t.size and t.dtype.kind not in "iu":
+        # the reference indexes its one-hot with them (functional.py:288-289)
+        if isinstance(targets, np.ndarray):
+            raise IndexError("arrays used as indices must be of integer (or boolean) type")
+        raise IndexError("only integers, slices (`:`), ellipsis (`...`), numpy.newaxis (`None`) and integer or "
+                         "boolean arrays are valid indices")
+    t = t.astype(np.int64).ravel()
     if len(t) != n:
         raise ValueError(f"{len(t)} targets for batch of {n}")
     bad = (t >= classes) | (t < -classes)

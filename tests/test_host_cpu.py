@@ -191,6 +191,11 @@ def test_cross_entropy_argument_checks(ox):
         F.cross_entropy(logits, [0, 1, 2])
     with pytest.raises(IndexError, match="out of bounds for axis 1 with size 3"):
         F.cross_entropy(logits, [0, 3])
+    # numpy's fancy indexing of the one-hot refuses float indices
+    with pytest.raises(IndexError, match="only integers"):
+        F.cross_entropy(logits, [0.0, 2.0])
+    with pytest.raises(IndexError, match="must be of integer"):
+        F.cross_entropy(logits, np.array([0.0, 2.0]))
 
 
 def test_boundary_buffer_checks(ox):
