@@ -165,8 +165,15 @@ __device__ __forceinline__ float act_vjp(float y, float g) {
   else return SiluBwd{}(y, g);
 }
 
+// Waves per SIMD the register budget must allow: the softmax positional-sum
+// split runs 4 blocks of 4 waves to a CU (at most 128 VGPRs); otherwise no
+// bound beyond the block size.
+template <bool LSUM, int ACT>
+constexpr int bwd_waves_per_eu() { return LSUM && is_softmax_act(ACT) ? 4 : 1; }
+
 template <int TPR, int NV, int MODE, bool LN, bool NTS, int ACT, bool LSUM>
-__global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM>())) void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
+__global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM>())) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu<LSUM, ACT>())))
+void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  const float* __restrict__ b,
                                                  const float* __restrict__ mean, const float* __restrict__ rstd,
                                                  const float* __restrict__ g, float* __restrict__ dyo,
@@ -367,7 +374,60 @@ __global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM>())) void norm_bwd_k(con
   float ia = 0.f, ma = 0.f, ib = 0.f, mb = 0.f;
   // The scheduling barriers keep the current row's first use below the next
   // row's loads, so its wait leaves those loads in flight.
-  if constexpr (LSUM) {
+  if constexpr (LSUM && is_softmax_act(ACT)) {
+    // Rows are (lead, T): row b * T + p is batch b at position p. The softmax
+    // prologue makes a row's VJP long, so a position's rows are spread over
+    // the block's waves rather than walked by one: a block owns positions
+    // p = block, block + blocks, ...; for each, wave gi forms the VJP of its
+    // contiguous share of the batch rows (each row reduced within one wave,
+    // as the node-by-node kernels do, so dx has their bits) and writes dx.
+    // After a barrier the block's threads take the row's columns, and each
+    // adds its column over the position's rows in batch order, starting from
+    // 0.0f, re-reading dx (just written by this CU: from L2): the sequential
+    // sum oxi_reduce(SUM) forms over the leading dim, bit for bit. One wave
+    // per position walking all its rows (below) runs this VJP at one wave
+    // per SIMD: 42-44 us at C5's (16, 1024, 768); split, 4 waves per SIMD at
+    // 118 VGPRs: 39-41 us; the pass without the positional sum: 33 us.
+    const int lead = (int)(rows / T);
+    const int q = (lead + GPB - 1) / GPB;  // rows of a position per wave
+    const int b0 = gi * q;
+    const int nb = max(0, min(lead, b0 + q) - b0);
+    for (int64_t p = blockIdx.x; p < T; p += gridDim.x) {
+      if (nb > 0) {
+        // two rows in flight; every prefetch issues (past the wave's last row
+        // it re-reads that row), so each wait counts exactly the younger loads
+        const int64_t r_first = (int64_t)b0 * T + p;
+        auto rj = [&](int j) { return r_first + (int64_t)min(j, nb - 1) * T; };
+        fetch(xa, ga, ia, ma, rj(0));
+        for (int j = 0; j < nb; j += 2) {
+          fetch(xb, gb, ib, mb, rj(j + 1));
+          __builtin_amdgcn_sched_barrier(0);
+          process(xa, ga, ia, ma, rj(j));
+          if (j + 1 >= nb) break;
+          fetch(xa, ga, ia, ma, rj(j + 2));
+          __builtin_amdgcn_sched_barrier(0);
+          process(xb, gb, ib, mb, rj(j + 1));
+        }
+      }
+      __syncthreads();  // every dx row of position p is written
+      for (int c = threadIdx.x; c < h4; c += NT) {
+        const f4* src = reinterpret_cast<const f4*>(dx + p * H) + c;
+        const int64_t step = T * (int64_t)h4;  // float4s from one batch row to the next
+        f4 acc = zero;
+        int bb = 0;
+        for (; bb + 4 <= lead; bb += 4) {
+          const f4 v0 = src[(int64_t)bb * step], v1 = src[(int64_t)(bb + 1) * step];
+          const f4 v2 = src[(int64_t)(bb + 2) * step], v3 = src[(int64_t)(bb + 3) * step];
+          acc = acc + v0;
+          acc = acc + v1;
+          acc = acc + v2;
+          acc = acc + v3;
+        }
+        for (; bb < lead; ++bb) acc = acc + src[(int64_t)bb * step];
+        st_stream<NTS>(acc, reinterpret_cast<f4*>(lsum + p * H) + c);
+      }
+    }
+  } else if constexpr (LSUM) {
     // Rows are (lead, T): row b * T + p is batch b at position p. Each wave
     // owns positions p = wave, wave + waves, ... and walks a position's rows
     // in batch order, LSUM_DEPTH rows in flight (the row sequence continues
@@ -701,9 +761,11 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   const int gpb = nt / tpr;
   // Blocks: enough to fill the chip, few enough that the partial rows stay
   // a small fraction of the row traffic.
-  int64_t nblk = lsum ? ceil_div(rows / lead, gpb) : ceil_div(rows, gpb);  // lsum: a wave per position
+  // lsum: a wave per position, or with a softmax a block per position
+  const bool split = lsum && is_softmax_act(ACT);
+  int64_t nblk = lsum ? (split ? rows / lead : ceil_div(rows / lead, gpb)) : ceil_div(rows, gpb);
   // (measured: 2 blocks per CU beat 3 and 4 for 4096-float rows)
-  const int64_t cap = (int64_t)cu_count() * (nt == 1024 ? 1 : 2);
+  const int64_t cap = (int64_t)cu_count() * (split ? 4 : nt == 1024 ? 1 : 2);
   if (need_part && nblk > cap) nblk = cap;
   if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
   if (nblk < 1) nblk = 1;
