@@ -143,8 +143,22 @@ __global__ __launch_bounds__(BS) void norm_fwd_loop_k(const float* __restrict__ 
 // blocks per CU) when 4 float4s per lane would not fit the registers of 16;
 // wider rows 1 per block. The leading-sum walk (LSUM) runs 4 waves to a
 // block, each with LSUM_DEPTH rows in flight.
-template <int TPR, int NV, bool LSUM = false>
-constexpr int bwd_threads() { return LSUM ? 256 : TPR == 64 ? (NV <= 3 ? 1024 : 512) : TPR; }
+// The softmax positional-sum split's block (waves per position) and whether
+// it loads x and g non-temporally. Measured at C5's (16, 1024, 768): 256
+// threads with plain loads 40.7 us; non-temporal loads 47.1 us; 512 and
+// 1024 threads (non-temporal) 47.4 and 52.0 us.
+#ifndef OXI_LSUM_SPLIT_THREADS
+#define OXI_LSUM_SPLIT_THREADS 256
+#endif
+#ifndef OXI_LSUM_SPLIT_NT
+#define OXI_LSUM_SPLIT_NT 0
+#endif
+constexpr int LSUM_SPLIT_THREADS = OXI_LSUM_SPLIT_THREADS;  // a position's waves with a softmax
+template <int TPR, int NV, bool LSUM = false, int ACT = OXI_ACT_NONE>
+constexpr int bwd_threads() {
+  return LSUM ? ((ACT == OXI_ACT_SOFTMAX || ACT == OXI_ACT_LOG_SOFTMAX) ? LSUM_SPLIT_THREADS : 256)
+              : TPR == 64 ? (NV <= 3 ? 1024 : 512) : TPR;
+}
 constexpr int LSUM_THREADS = 256;
 #ifndef OXI_LSUM_DEPTH
 #define OXI_LSUM_DEPTH 4
@@ -172,7 +186,7 @@ template <bool LSUM, int ACT>
 constexpr int bwd_waves_per_eu() { return LSUM && is_softmax_act(ACT) ? 4 : 1; }
 
 template <int TPR, int NV, int MODE, bool LN, bool NTS, int ACT, bool LSUM>
-__global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM>())) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu<LSUM, ACT>())))
+__global__ __launch_bounds__((bwd_threads<TPR, NV, LSUM, ACT>())) __attribute__((amdgpu_waves_per_eu(bwd_waves_per_eu<LSUM, ACT>())))
 void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  const float* __restrict__ b,
                                                  const float* __restrict__ mean, const float* __restrict__ rstd,
@@ -181,7 +195,7 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  float* __restrict__ part, int64_t rows, int H,
                                                  float* __restrict__ lsum, int64_t T) {
   static_assert(!LSUM || TPR == 64, "the leading-sum walk takes one-wave rows");
-  constexpr int NT = bwd_threads<TPR, NV, LSUM>();
+  constexpr int NT = bwd_threads<TPR, NV, LSUM, ACT>();
   constexpr int GPB = NT / TPR;
   constexpr int ROWF = TPR * NV * 4;  // floats a group covers
   __shared__ float lds[2 * (NT / 64)];
@@ -249,8 +263,9 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
     // the lead-sum walk's last refills re-read a row it has just read: plain
     // loads keep it in L2 (non-temporal ones fetched it from HBM again, +25%
     // reads at 16 rows a position)
-    xt.template load_clamped<!LSUM>(x + r * H, h4, t);
-    gt.template load_clamped<!LSUM>(g + r * H, h4, t);
+    constexpr bool ntl = !LSUM || (is_softmax_act(ACT) && OXI_LSUM_SPLIT_NT);
+    xt.template load_clamped<ntl>(x + r * H, h4, t);
+    gt.template load_clamped<ntl>(g + r * H, h4, t);
     inv = rstd[r];
     if constexpr (LN) mu = mean[r];
   };
@@ -698,7 +713,7 @@ void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x
     break;
 #define OXI_BWD_LSUM(NV)                                                                                   \
   case 640 + NV:                                                                                           \
-    norm_bwd_k<64, NV, MODE, LN, NTS, ACT, true><<<dim3((unsigned)nblk), dim3(LSUM_THREADS), 0, s>>>(      \
+    norm_bwd_k<64, NV, MODE, LN, NTS, ACT, true><<<dim3((unsigned)nblk), dim3(bwd_threads<64, NV, true, ACT>()), 0, s>>>( \
         x, w, b, mean, rstd, g, dyo, dx, part, rows, h, lsum, T);                                          \
     break;
   if (lsum) {  // one-wave rows only (lsum_check)
@@ -757,15 +772,15 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   const int cfg = vec_ok(H, {x, w, b, g, dyo, dx}) ? pick_bwd_cfg(H / 4) : 0;
   if (ACT != ACT_NONE && cfg == 0) return fail(OXI_OTHER, "norm_act_bwd: internal: unvectorized fused launch");
   const int tpr = cfg ? cfg / 10 : BS;
-  const int nt = lsum ? LSUM_THREADS : tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : tpr;  // bwd_threads<>()
+  const bool split = lsum && is_softmax_act(ACT);
+  const int nt = lsum ? (split ? LSUM_SPLIT_THREADS : LSUM_THREADS) : tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : tpr;  // bwd_threads<>()
   const int gpb = nt / tpr;
   // Blocks: enough to fill the chip, few enough that the partial rows stay
   // a small fraction of the row traffic.
   // lsum: a wave per position, or with a softmax a block per position
-  const bool split = lsum && is_softmax_act(ACT);
   int64_t nblk = lsum ? (split ? rows / lead : ceil_div(rows / lead, gpb)) : ceil_div(rows, gpb);
   // (measured: 2 blocks per CU beat 3 and 4 for 4096-float rows)
-  const int64_t cap = (int64_t)cu_count() * (split ? 4 : nt == 1024 ? 1 : 2);
+  const int64_t cap = (int64_t)cu_count() * (split ? 1024 / LSUM_SPLIT_THREADS : nt == 1024 ? 1 : 2);
   if (need_part && nblk > cap) nblk = cap;
   if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
   if (nblk < 1) nblk = 1;
