@@ -780,7 +780,11 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   // lsum: a wave per position, or with a softmax a block per position
   int64_t nblk = lsum ? (split ? rows / lead : ceil_div(rows / lead, gpb)) : ceil_div(rows, gpb);
   // (measured: 2 blocks per CU beat 3 and 4 for 4096-float rows)
-  const int64_t cap = (int64_t)cu_count() * (split ? 1024 / LSUM_SPLIT_THREADS : nt == 1024 ? 1 : 2);
+  // blocks per CU of the split (2, 3, 4 at C5: 40.4, 40.1, 40.2 us)
+#ifndef OXI_LSUM_SPLIT_BPC
+#define OXI_LSUM_SPLIT_BPC (1024 / LSUM_SPLIT_THREADS)
+#endif
+  const int64_t cap = (int64_t)cu_count() * (split ? OXI_LSUM_SPLIT_BPC : nt == 1024 ? 1 : 2);
   if (need_part && nblk > cap) nblk = cap;
   if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
   if (nblk < 1) nblk = 1;
