@@ -1088,7 +1088,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (asked for --gpus {args.gpus}); the row-sharded multi-GPU "
-              "design is described in DESIGN.md and not built", file=sys.stderr)
+              "path is not built", file=sys.stderr)
         sys.exit(2)
     from oxitorch_amd import capi as hip
 
@@ -1125,7 +1125,7 @@ def main():
         "gbs_definitions": ("value/gbs/pct_of_peak: the HBM bytes the step's kernels move (per C-ABI call, checked "
                             "against rocprofv3 FETCH_SIZE + WRITE_SIZE in profiles/pmc_traffic_<config>.md) over "
                             "the step's time, against the 8 TB/s peak. per_op_gbs/per_op_pct_of_peak: the per-op "
-                            "algorithmic bytes of BASELINE.md (each F.* op reading its inputs and writing its "
+                            "algorithmic bytes of the metric (each F.* op reading its inputs and writing its "
                             "outputs once) over the same time, the rate a step of separate ops would need; it passes "
                             "the peak where the fused passes remove traffic. roofline: the dominant call alone"),
         "rows_per_s": head["rows_per_s"],
