@@ -422,15 +422,22 @@ __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict_
 #endif
 constexpr int SEG_U = OXI_SEG_U;
 constexpr int ZR = 4;
+// Waves per SIMD the segment kernel is held to: at 5 it fits 84 VGPRs with no
+// spill (unbounded, the compiler takes 120: 4 waves). Measured: C5's
+// embedding VJP 35.8-36.1 us against 38.5-38.8; C4's unchanged (145-148 us).
+// At 6 and 8 it spills 4 and 24 VGPRs. Segment blocks spread evenly among the
+// zero-row blocks (instead of first) measured 42-46 us on C5, 147-149 on C4.
+#ifndef OXI_SEG_WPE
+#define OXI_SEG_WPE 5
+#endif
 
 template <bool VEC, bool NTS>
-__global__ __launch_bounds__(256) void seg_wave_k(const float* __restrict__ g, int64_t outer, int64_t n,
-                                                  int64_t inner, int64_t len, const int* __restrict__ skeys,
-                                                  const int* __restrict__ perm, float* __restrict__ grad,
-                                                  float* __restrict__ part, const int* __restrict__ present,
-                                                  int* __restrict__ owners, int* __restrict__ owner_count,
-                                                  int* __restrict__ end_tile, int st, int64_t stiles, int chunks,
-                                                  int64_t seg_blocks) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE))) void seg_wave_k(
+    const float* __restrict__ g, int64_t outer, int64_t n, int64_t inner, int64_t len,
+    const int* __restrict__ skeys, const int* __restrict__ perm, float* __restrict__ grad,
+    float* __restrict__ part, const int* __restrict__ present, int* __restrict__ owners,
+    int* __restrict__ owner_count, int* __restrict__ end_tile, int st, int64_t stiles, int chunks,
+    int64_t seg_blocks) {
   using V = typename std::conditional<VEC, f4, float>::type;
   const int64_t units = VEC ? inner / 4 : inner;
   if ((int64_t)blockIdx.x >= seg_blocks) {
