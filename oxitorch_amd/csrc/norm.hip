@@ -744,6 +744,17 @@ void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x
 #undef OXI_BWD_LSUM
 }
 
+// 1024-thread (one-wave row) blocks per CU: 2 made C5's layer_norm + silu
+// VJP 43 us against 35 us at 1 (C1's rms_norm VJP unchanged)
+#ifndef OXI_BWD_BPC1024
+#define OXI_BWD_BPC1024 1
+#endif
+// Blocks per CU of a backward launch of nt-thread blocks that writes column
+// partials (the softmax positional-sum split aside); the partial buffer's
+// size and the launch both come from it. (measured: 2 blocks per CU beat 3
+// and 4 for 4096-float rows)
+constexpr int bwd_blocks_per_cu(int nt) { return nt == 1024 ? OXI_BWD_BPC1024 : 2; }
+
 // Bytes of column partials the backward needs for (rows, H): 2 x blocks x H
 // floats, or 0 when neither dw nor db is wanted.
 size_t bwd_part_bytes(bool need_part, int64_t rows, int64_t H, int cfg) {
@@ -751,22 +762,22 @@ size_t bwd_part_bytes(bool need_part, int64_t rows, int64_t H, int cfg) {
   const int tpr = cfg ? cfg / 10 : BS;
   const int nt = tpr == 64 ? (cfg % 10 <= 3 ? 1024 : 512) : tpr;  // bwd_threads<TPR, NV>()
   int64_t nblk = ceil_div(rows, nt / tpr);
-  const int64_t cap = (int64_t)cu_count() * (nt == 1024 ? 1 : 2);
+  const int64_t cap = (int64_t)cu_count() * bwd_blocks_per_cu(nt);
   if (nblk > cap) nblk = cap;
   if (nblk < 1) nblk = 1;
   return sizeof(float) * 2 * (size_t)nblk * (size_t)H;
 }
 
-// `fixed` (when not null) holds at least bwd_part_bytes() bytes of device
-// memory for the column partials; otherwise they come from the caching
-// allocator.
+// `fixed` (when not null) is fixed_bytes of device memory for the column
+// partials, which must hold bwd_part_bytes() (checked before any launch);
+// otherwise they come from the caching allocator.
 // lsum (with lead > 0): also write lsum (rows / lead, H) = the sum of dx over
 // the leading dim of a (lead, rows / lead) row grid; the caller has checked
 // lsum_ok().
 template <bool LN, int MODE, int ACT = ACT_NONE>
 int launch_bwd(const float* x, const float* w, const float* b, const float* mean, const float* rstd,
                const float* g, float* dyo, float* dx, float* dw, float* db, int64_t rows, int64_t H,
-               void* fixed = nullptr, float* lsum = nullptr, int64_t lead = 0) {
+               void* fixed = nullptr, float* lsum = nullptr, int64_t lead = 0, size_t fixed_bytes = 0) {
   hipStream_t s = stream();
   const bool need_part = dw || (LN && db);
   const int cfg = vec_ok(H, {x, w, b, g, dyo, dx}) ? pick_bwd_cfg(H / 4) : 0;
@@ -779,21 +790,19 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   // a small fraction of the row traffic.
   // lsum: a wave per position, or with a softmax a block per position
   int64_t nblk = lsum ? (split ? rows / lead : ceil_div(rows / lead, gpb)) : ceil_div(rows, gpb);
-  // (measured: 2 blocks per CU beat 3 and 4 for 4096-float rows)
   // blocks per CU of the split (2, 3, 4 at C5: 40.4, 40.1, 40.2 us)
 #ifndef OXI_LSUM_SPLIT_BPC
 #define OXI_LSUM_SPLIT_BPC (1024 / LSUM_SPLIT_THREADS)
 #endif
-  // 1024-thread (one-wave row) blocks per CU: 2 made C5's layer_norm + silu
-  // VJP 43 us against 35 us at 1 (C1's rms_norm VJP unchanged)
-#ifndef OXI_BWD_BPC1024
-#define OXI_BWD_BPC1024 1
-#endif
-  const int64_t cap = (int64_t)cu_count() * (split ? OXI_LSUM_SPLIT_BPC : nt == 1024 ? OXI_BWD_BPC1024 : 2);
+  const int64_t cap = (int64_t)cu_count() * (split ? OXI_LSUM_SPLIT_BPC : bwd_blocks_per_cu(nt));
   if (need_part && nblk > cap) nblk = cap;
   if (!need_part && nblk > (int64_t)cu_count() * 16) nblk = (int64_t)cu_count() * 16;
   if (nblk < 1) nblk = 1;
-  Workspace ws(need_part && !fixed ? sizeof(float) * 2 * (size_t)nblk * (size_t)H : 0);
+  const size_t part_bytes = need_part ? sizeof(float) * 2 * (size_t)nblk * (size_t)H : 0;
+  if (fixed && part_bytes > fixed_bytes)
+    return fail(OXI_OTHER, "norm VJP: internal: column partials of %zu bytes exceed the fixed buffer of %zu bytes",
+                part_bytes, fixed_bytes);
+  Workspace ws(!fixed ? part_bytes : 0);
   if (need_part && !fixed && !ws.p) return fail_alloc("norm VJP: column partials");
   // no partials without dw/db: the kernel then writes none (its launch shape
   // may have more blocks than bwd_part_bytes() sizes for)
@@ -967,9 +976,10 @@ int oxi_layer_norm_bwd_noalloc(const float* x, const float* w, const float* mean
   if (!sp) return fail(OXI_OTHER, "layer_norm_bwd_noalloc: no scratch address for the bound device");
   std::lock_guard<std::mutex> lk(noalloc_mutex());
   return mode == OXI_NORM_VJP_REF
-             ? launch_bwd<true, OXI_NORM_VJP_REF>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols, sp)
+             ? launch_bwd<true, OXI_NORM_VJP_REF>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols, sp,
+                                                  nullptr, 0, (size_t)OXI_NOALLOC_SCRATCH_BYTES)
              : launch_bwd<true, OXI_NORM_VJP_EXACT>(x, w, nullptr, mean, rstd, g, nullptr, dx, dw, db, rows, cols,
-                                                    sp);
+                                                    sp, nullptr, 0, (size_t)OXI_NOALLOC_SCRATCH_BYTES);
 }
 
 int oxi_rms_norm_bwd_lead_sum(const float* x, const float* w, const float* rstd, const float* g, int act, float* dy,
