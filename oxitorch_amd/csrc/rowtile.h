@@ -61,7 +61,9 @@ constexpr int row_block_threads(int tpr) { return (256 % tpr == 0) ? 256 : tpr; 
 // not fit in registers. Rows keep several float4s per lane: measured on
 // MI355X, one float4 per lane (192 threads per 768-float row, 1024 per
 // 4096-float row) made the layer-norm forward 30% slower, the block-wide
-// reductions over many waves costing more than the access pattern gains.
+// reductions over many waves costing more than the access pattern gains;
+// 512 x 2 for a 4096-float row measured the same as 256 x 4 (layer-norm
+// forward at (16384, 4096): 88.8-89.5 us against 87.7-89.3 us).
 inline int pick_row_cfg(int64_t h4) {
   if (h4 <= 64) return 641;
   if (h4 <= 128) return 642;
