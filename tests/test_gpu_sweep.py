@@ -12,10 +12,11 @@ order, the sum moves an output near zero by more than that bar (a
 log-probability of -0.009 at a row's dominant element, -log(s) with s the
 sum of 1026 exponentials, came out 2.95e-6 from the f32 oracle), so an
 element outside it must be no further from float64 than the reference
-path's own worst element. The embedding gather and its VJP get the same
-treatment over table widths and id distributions: the gather bit-exact, each
-id's run that lies inside one position tile bit-exact, absent rows +0, long
-sums against float64.
+path's own worst element. At every width the fused norm + activation VJPs
+must give the node-by-node VJPs' bits, or refuse the width. The embedding
+gather and its VJP get the same treatment over table widths and id
+distributions: the gather bit-exact, each id's run that lies inside one
+position tile bit-exact, absent rows +0, long sums against float64.
 """
 
 import sys
@@ -151,6 +152,55 @@ def test_sweep_cross_entropy(hip, R, H):
     assert_close_arb(d * R, want_d, exact_d, what=f"n*dlogits (bwd) {R}x{H}")
     if d2 is not None:
         assert_close_arb(d2.numpy() * R, want_d, exact_d, what=f"n*dlogits (one pass) {R}x{H}")
+
+
+FUSED_ACTS = ["gelu_tanh", "gelu_erf", "silu", "softmax", "log_softmax"]
+
+
+def _act_bwd(hip, y, g, act):
+    if act in ("softmax", "log_softmax"):
+        log = act == "log_softmax"
+        return hip.softmax_bwd(hip.softmax_fwd(y, log=log), g, log=log)
+    if act == "silu":
+        return hip.silu_bwd(y, g)
+    return hip.gelu_bwd(y, g, "tanh" if act == "gelu_tanh" else "none")
+
+
+def _same(a, b, what):
+    a, b = a.numpy(), b.numpy()
+    assert a.shape == b.shape, what
+    bad = np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))
+    assert bad.size == 0, f"{what}: {bad.size} of {a.size} differ, first at {bad[0]}: {a.flat[bad[0]]} vs {b.flat[bad[0]]}"
+
+
+@pytest.mark.parametrize("R,H", CASES, ids=[f"{R}x{H}" for R, H in CASES])
+def test_sweep_fused_norm_act(hip, R, H):
+    """The fused norm + activation VJPs give the node-by-node VJPs' bits
+    (dy, dx, dw, db) at every width they take: a multiple of 4 floats up to
+    8192, up to 2048 with a softmax. Other widths are refused."""
+    say("sweep fused norm+act", R, H)
+    x, w, b, g = _data(R * 19 + H, R, H)
+    dx_, dw_, db_, dg = D(hip, x), D(hip, w), D(hip, b), D(hip, g)
+    y, mean, rstd = hip.layer_norm_fwd(dx_, dw_, db_, 1e-5)
+    yr, rstd_r = hip.rms_norm_fwd(dx_, dw_, 1e-6)
+    for act in FUSED_ACTS:
+        soft = act in ("softmax", "log_softmax")
+        if H % 4 or H > (2048 if soft else 8192):
+            with pytest.raises(NotImplementedError):
+                hip.layer_norm_act_bwd(dx_, dw_, db_, mean, rstd, dg, act)
+            with pytest.raises(NotImplementedError):
+                hip.rms_norm_act_bwd(dx_, dw_, rstd_r, dg, act)
+            continue
+        dy2 = _act_bwd(hip, y, dg, act)
+        dx2, dw2, db2 = hip.layer_norm_bwd(dx_, dw_, mean, rstd, dy2)
+        dy, dx, dw, db = hip.layer_norm_act_bwd(dx_, dw_, db_, mean, rstd, dg, act)
+        for name, a, c in (("dy", dy, dy2), ("dx", dx, dx2), ("dw", dw, dw2), ("db", db, db2)):
+            _same(a, c, f"layer_norm+{act} {name} {R}x{H}")
+        dyr2 = _act_bwd(hip, yr, dg, act)
+        dxr2, dwr2 = hip.rms_norm_bwd(dx_, dw_, rstd_r, dyr2)
+        dyr, dxr, dwr = hip.rms_norm_act_bwd(dx_, dw_, rstd_r, dg, act)
+        for name, a, c in (("dy", dyr, dyr2), ("dx", dxr, dxr2), ("dw", dwr, dwr2)):
+            _same(a, c, f"rms_norm+{act} {name} {R}x{H}")
 
 
 def _exact_bwd(g, L, idx):
