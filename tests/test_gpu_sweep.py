@@ -16,7 +16,10 @@ path's own worst element. At every width the fused norm + activation VJPs
 must give the node-by-node VJPs' bits, or refuse the width. The embedding
 gather and its VJP get the same treatment over table widths and id
 distributions: the gather bit-exact, each id's run that lies inside one
-position tile bit-exact, absent rows +0, long sums against float64.
+position tile bit-exact, absent rows +0, long sums against float64. Last,
+seeded random shapes of rank 1 to 4 take every dim reduction over one dim of
+a contiguous or permuted view, and every binary op over operands with
+broadcast dims, fewer leading dims and a permuted storage order.
 """
 
 import sys
@@ -241,3 +244,102 @@ def test_sweep_embedding(hip, V, Dm, n, dist):
     absent = np.bincount(keys, minlength=V) == 0
     assert not dW[absent].any(), "rows of ids that never occur must be zero"
     assert_reduction_close(dW, want32, _exact_bwd(g, V, ids), what=f"embedding dW {V}x{Dm} n={n} {dist}")
+
+
+# ---- dim reductions and the binary registry over random strided shapes -------------------------
+
+def _red_cases():
+    r = rng(77)
+    out = []
+    for _ in range(24):
+        nd = int(r.integers(1, 5))
+        shape = tuple(int(s) for s in r.integers(1, 41 if nd < 4 else 13, nd))
+        out.append((shape, int(r.integers(0, nd)), bool(r.integers(0, 2))))
+    return out
+
+
+RED_CASES = _red_cases()
+
+
+@pytest.mark.parametrize("shape,dim,permuted", RED_CASES,
+                         ids=[f"{'x'.join(map(str, s))}-d{d}{'-perm' if p else ''}" for s, d, p in RED_CASES])
+def test_sweep_reduce(hip, shape, dim, permuted):
+    """Every reduction kind over one dim of a contiguous or permuted view:
+    max, min, argmax and argmin bit-exact (first winner); sum, mean and norm
+    against the oracle with float64 as the arbiter."""
+    from oracle import ref
+    say("sweep reduce", shape, dim, permuted)
+    r = rng(sum(shape) * 31 + dim)
+    nd = len(shape)
+    if permuted and nd > 1:
+        perm = tuple(int(p) for p in r.permutation(nd))
+        base = r.standard_normal(tuple(shape[p] for p in perm)).astype(np.float32)  # stored layout
+        view = base.transpose(np.argsort(perm))  # logical layout `shape`
+    else:
+        base = r.standard_normal(shape).astype(np.float32)
+        view = base
+    strides = [s // 4 for s in view.strides]
+    x = np.ascontiguousarray(view)
+    x64 = x.astype(np.float64)
+    exact = {"sum": x64.sum(dim), "mean": x64.mean(dim), "norm": np.sqrt((x64 * x64).sum(dim))}
+    for kind in ("sum", "mean", "max", "min", "argmax", "argmin", "norm"):
+        got = hip.reduce(kind, D(hip, base), dim, x_strides=strides, shape=shape).numpy()
+        want = ref.reduce(kind, x, dim)
+        if kind in exact:
+            assert_close_arb(got, want, exact[kind], what=f"reduce {kind} {shape} dim {dim}")
+        else:
+            np.testing.assert_array_equal(got, want, err_msg=f"reduce {kind} {shape} dim {dim}")
+
+
+def _bin_cases():
+    r = rng(91)
+    out = []
+    for _ in range(16):
+        nd = int(r.integers(1, 5))
+        shape = tuple(int(s) for s in r.integers(1, 31 if nd < 4 else 11, nd))
+        a_keep = tuple(bool(k) for k in r.integers(0, 4, nd) > 0)  # False: size 1, broadcast
+        b_keep = tuple(bool(k) for k in r.integers(0, 3, nd) > 0)
+        b_lead = int(r.integers(0, nd))  # leading dims b does not have
+        out.append((shape, a_keep, b_keep, b_lead, bool(r.integers(0, 2))))
+    return out
+
+
+BIN_CASES = _bin_cases()
+BIN_OPS = ["add", "sub", "mul", "div", "pow", "min", "max", "eq", "ne", "lt", "le", "gt", "ge"]
+
+
+@pytest.mark.parametrize("shape,a_keep,b_keep,b_lead,a_perm", BIN_CASES,
+                         ids=[f"case{i}" for i in range(len(BIN_CASES))])
+def test_sweep_binary(hip, shape, a_keep, b_keep, b_lead, a_perm):
+    """Every binary op over broadcast operands: a with size-1 dims and
+    optionally stored permuted, b with size-1 dims and fewer leading dims.
+    Results bit-exact (IEEE add, sub, mul, correctly rounded div, min, max,
+    comparisons) except pow, to 2e-6 relative."""
+    from oracle import ref
+    say("sweep binary", shape, a_keep, b_keep, b_lead, a_perm)
+    r = rng(sum(shape) * 37 + b_lead)
+    nd = len(shape)
+    a_shape = tuple(s if k else 1 for s, k in zip(shape, a_keep))
+    if a_perm and nd > 1:
+        perm = tuple(int(p) for p in r.permutation(nd))
+        a_base = r.standard_normal(tuple(a_shape[p] for p in perm)).astype(np.float32)
+        a_view = a_base.transpose(np.argsort(perm))
+    else:
+        a_base = r.standard_normal(a_shape).astype(np.float32)
+        a_view = a_base
+    b_shape = tuple(s if k else 1 for s, k in zip(shape, b_keep))[b_lead:]
+    b = r.standard_normal(b_shape).astype(np.float32)
+    a_str = [s // 4 for s in np.broadcast_to(a_view, shape).strides]
+    b_str = [s // 4 for s in np.broadcast_to(b, shape).strides]
+    a_c = np.ascontiguousarray(a_view)
+    da, db = D(hip, a_base), D(hip, b)
+    for op in BIN_OPS:
+        aa = np.abs(a_c) + 0.1 if op == "pow" else a_c
+        dA = D(hip, np.abs(a_base) + 0.1) if op == "pow" else da
+        got = hip.binary(op, dA, db, a_str, b_str, shape).numpy()
+        # the output shape, also along dims that neither operand covers
+        want = ref.binary(op, np.broadcast_to(aa, shape), np.broadcast_to(b, shape))
+        if op == "pow":
+            assert_close(got, want, rtol=2e-6, what=f"binary pow {shape}")
+        else:
+            np.testing.assert_array_equal(got, want, err_msg=f"binary {op} {shape}")
