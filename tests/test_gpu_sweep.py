@@ -19,7 +19,8 @@ distributions: the gather bit-exact, each id's run that lies inside one
 position tile bit-exact, absent rows +0, long sums against float64. Last,
 seeded random shapes of rank 1 to 4 take every dim reduction over one dim of
 a contiguous or permuted view, and every binary op over operands with
-broadcast dims, fewer leading dims and a permuted storage order.
+broadcast dims, fewer leading dims and a permuted storage order; softmax and
+log_softmax over any dim; gelu and silu with x and g on permuted views.
 """
 
 import sys
@@ -343,3 +344,74 @@ def test_sweep_binary(hip, shape, a_keep, b_keep, b_lead, a_perm):
             assert_close(got, want, rtol=2e-6, what=f"binary pow {shape}")
         else:
             np.testing.assert_array_equal(got, want, err_msg=f"binary {op} {shape}")
+
+
+# ---- softmax over any dim, activations over permuted views ---------------------------------------
+
+def _dim_cases():
+    r = rng(113)
+    out = []
+    for _ in range(16):
+        nd = int(r.integers(2, 5))
+        shape = tuple(int(s) for s in r.integers(1, 70 if nd == 2 else (25 if nd == 3 else 12), nd))
+        out.append((shape, int(r.integers(0, nd))))
+    return out
+
+
+DIM_CASES = _dim_cases()
+
+
+@pytest.mark.parametrize("shape,dim", DIM_CASES, ids=[f"{'x'.join(map(str, s))}-d{d}" for s, d in DIM_CASES])
+def test_sweep_softmax_any_dim(hip, shape, dim):
+    """softmax / log_softmax over a leading, middle or last dim (inner > 1
+    for all but the last), forward and VJP, arbitrated by float64."""
+    from oracle import ref, closed_form
+    say("sweep softmax dim", shape, dim)
+    r = rng(sum(shape) * 41 + dim)
+    x = (r.standard_normal(shape, dtype=np.float32) * 3).astype(np.float32)
+    g = r.standard_normal(shape, dtype=np.float32)
+    for log in (False, True):
+        name = "log_softmax" if log else "softmax"
+        y = hip.softmax_fwd(D(hip, x), dim, log=log).numpy()
+        want = ref.log_softmax_fwd(x, dim) if log else ref.softmax_fwd(x, dim)
+        exact = closed_form.log_softmax(x, dim) if log else closed_form.softmax(x, dim)
+        assert_close_arb(y, want, exact, what=f"{name} {shape} dim {dim}")
+        d = hip.softmax_bwd(D(hip, y), D(hip, g), dim, log=log).numpy()
+        want_d = ref.log_softmax_bwd(x, g, dim) if log else ref.softmax_bwd(x, g, dim)
+        exact_d = closed_form.log_softmax_bwd(x, g, dim) if log else closed_form.softmax_bwd(x, g, dim)
+        assert_close_arb(d, want_d, exact_d, what=f"{name} bwd {shape} dim {dim}")
+
+
+def _view(r, shape):
+    """A permuted view of shape `shape`: (stored array, its element strides)."""
+    nd = len(shape)
+    perm = tuple(int(p) for p in r.permutation(nd))
+    base = (r.standard_normal(tuple(shape[p] for p in perm), dtype=np.float32) * 3).astype(np.float32)
+    view = base.transpose(np.argsort(perm))
+    return base, view, [s // 4 for s in view.strides]
+
+
+@pytest.mark.parametrize("shape,dim", DIM_CASES, ids=[f"{'x'.join(map(str, s))}-{i}" for i, (s, _) in enumerate(DIM_CASES)])
+def test_sweep_activations_on_views(hip, shape, dim):
+    """gelu (tanh, exact erf) and silu, forward and VJP, with x and g each a
+    differently permuted view: tanh-GELU and SiLU against the oracle, the
+    exact-erf GELU (which the reference lacks) against float64."""
+    from oracle import ref, closed_form
+    say("sweep activations on views", shape)
+    r = rng(sum(shape) * 43 + dim)
+    xb, xv, xs = _view(r, shape)
+    gb, gv, gs = _view(r, shape)
+    x, g = np.ascontiguousarray(xv), np.ascontiguousarray(gv)
+    dxb, dgb = D(hip, xb), D(hip, gb)
+    y = hip.gelu_fwd(dxb, "tanh", x_strides=xs, shape=shape).numpy()
+    assert_close(y, ref.gelu_tanh_fwd(x), what=f"gelu tanh {shape}")
+    d = hip.gelu_bwd(dxb, dgb, "tanh", x_strides=xs, g_strides=gs, shape=shape).numpy()
+    assert_close(d, ref.gelu_tanh_bwd(x, g), what=f"gelu tanh bwd {shape}")
+    y = hip.gelu_fwd(dxb, "none", x_strides=xs, shape=shape).numpy()
+    assert_close(y, closed_form.gelu_erf(x), what=f"gelu erf {shape}")
+    d = hip.gelu_bwd(dxb, dgb, "none", x_strides=xs, g_strides=gs, shape=shape).numpy()
+    assert_close(d, closed_form.gelu_erf_grad(x) * g, what=f"gelu erf bwd {shape}")
+    y = hip.silu_fwd(dxb, x_strides=xs, shape=shape).numpy()
+    assert_close(y, ref.silu_fwd(x), what=f"silu {shape}")
+    d = hip.silu_bwd(dxb, dgb, x_strides=xs, g_strides=gs, shape=shape).numpy()
+    assert_close(d, ref.silu_bwd(x, g), what=f"silu bwd {shape}")
