@@ -9,7 +9,9 @@ VJP, then the LayerNorm VJP through the no-alloc entry point. It is replayed
 four times. Between replays the test uploads new inputs into the captured
 buffers and runs the same step eagerly through the allocating entry points,
 with host synchronisations in between. Every replay's outputs must equal the
-eager step's bit for bit. No call inside the capture allocates, copies,
+eager step's bit for bit. A second step captures the other workspace-free
+families the same way: a norm forward, softmax forward and VJP, a dim
+reduction and an AdamW step. No call inside the capture allocates, copies,
 clears memory or waits.
 """
 
@@ -102,6 +104,81 @@ def test_c2_step_replayed_from_a_hip_graph(hip):
                 bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
                 assert bad.size == 0, f"replay {k}: {name} differs from the eager step at {bad.size} elements"
             assert np.isfinite(E["dx"].numpy()).all()
+    finally:
+        if exe.value:
+            rt.hipGraphExecDestroy(exe)
+        rt.hipGraphDestroy(graph)
+
+
+def test_norm_softmax_reduce_optimizer_step_replayed_from_a_hip_graph(hip):
+    """The other workspace-free families in one captured step: rms_norm
+    forward, softmax forward and VJP over the rows, the column sum of the
+    VJP (a dim reduction), and an AdamW step on a parameter with that sum as
+    its gradient (m and v updated in place, reset to the same state before
+    each replay and each eager step). Every replay equals the eager step bit
+    for bit, the updated moments included."""
+    R, H = 1024, 768
+    say("hip graph: rms_norm, softmax, reduce, adamw", (R, H))
+    rt = _runtime()
+    A = hip.DeviceArray
+    r = rng(32)
+    x, g = A((R, H)), A((R, H))
+    w = hip.DeviceArray.from_numpy((r.standard_normal(H, dtype=np.float32) * 0.02 + 1).astype(np.float32))
+    P = hip.DeviceArray.from_numpy(r.standard_normal(H, dtype=np.float32))
+    m0 = (r.standard_normal(H, dtype=np.float32) * 0.01).astype(np.float32)
+    v0 = np.abs(r.standard_normal(H, dtype=np.float32) * 0.01).astype(np.float32)
+
+    def outputs():
+        return dict(y=A((R, H)), rstd=A((R,)), p=A((R, H)), dp=A((R, H)), s=A((H,)), m=A((H,)), v=A((H,)),
+                    Pn=A((H,)))
+
+    G, E = outputs(), outputs()
+    rm = hip._i64arr([H, 1])
+    shape = hip._i64arr([R, H])
+    SUM = hip.REDUCE.index("sum")
+
+    def step(o):
+        hip.call("oxi_rms_norm_fwd", x.ptr, w.ptr, o["y"].ptr, o["rstd"].ptr, R, H, ctypes.c_float(1e-6))
+        hip.call("oxi_softmax_fwd", o["y"].ptr, o["p"].ptr, R, H, 1)
+        hip.call("oxi_softmax_bwd", o["p"].ptr, g.ptr, o["dp"].ptr, R, H, 1)
+        hip.call("oxi_reduce", SUM, o["dp"].ptr, rm, shape, 2, 0, o["s"].ptr)
+        hip.call("oxi_adamw_step", P.ptr, o["s"].ptr, o["m"].ptr, o["v"].ptr, o["Pn"].ptr, H, 1e-3, 0.9, 0.999,
+                 1e-8, 1e-2, 1, 3)
+
+    def reset(o):
+        hip.check(hip.lib.oxi_hip_memcpy_h2d(o["m"].ptr, m0.ctypes.data, o["m"].nbytes))
+        hip.check(hip.lib.oxi_hip_memcpy_h2d(o["v"].ptr, v0.ctypes.data, o["v"].nbytes))
+
+    stream = ctypes.c_void_p()
+    hip.check(hip.lib.oxi_hip_stream(ctypes.byref(stream)))
+    hip.sync()
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamBeginCapture(stream, CAPTURE_MODE_RELAXED) == 0
+    try:
+        step(G)
+    finally:
+        rc_end = rt.hipStreamEndCapture(stream, ctypes.byref(graph))
+    assert rc_end == 0 and graph.value
+    try:
+        assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for k in range(4):
+            say("hip graph replay", k)
+            rk = rng(200 + k)
+            xs = (rk.standard_normal((R, H), dtype=np.float32) * (1 + k)).astype(np.float32)
+            gs = rk.standard_normal((R, H), dtype=np.float32)
+            hip.check(hip.lib.oxi_hip_memcpy_h2d(x.ptr, xs.ctypes.data, x.nbytes))
+            hip.check(hip.lib.oxi_hip_memcpy_h2d(g.ptr, gs.ctypes.data, g.nbytes))
+            reset(E)
+            step(E)
+            reset(G)
+            hip.sync()
+            assert rt.hipGraphLaunch(exe, stream) == 0
+            hip.sync()
+            for name in G:
+                got, want = G[name].numpy(), E[name].numpy()
+                bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+                assert bad.size == 0, f"replay {k}: {name} differs from the eager step at {bad.size} elements"
+            assert not np.array_equal(E["m"].numpy(), m0), "the step must move the first moment"
     finally:
         if exe.value:
             rt.hipGraphExecDestroy(exe)
