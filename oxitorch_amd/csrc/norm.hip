@@ -164,6 +164,16 @@ constexpr int LSUM_THREADS = 256;
 #define OXI_LSUM_DEPTH 4
 #endif
 constexpr int LSUM_DEPTH = OXI_LSUM_DEPTH;
+// The softmax positional-sum split stages a position's dx rows (lead x H
+// floats) in dynamic LDS when they take at most LSUM_STAGE_MAX bytes (one
+// block within 64 KB of LDS with its static arrays); larger positions are
+// re-read from dx.
+#ifndef OXI_LSUM_STAGE_MAX
+#define OXI_LSUM_STAGE_MAX (56 << 10)
+#endif
+__host__ __device__ constexpr bool lsum_staged(int64_t lead, int64_t H) {
+  return lead * H * 4 <= OXI_LSUM_STAGE_MAX;
+}
 
 // ACT_NONE: g is the norm output's gradient. Otherwise g is the gradient of
 // act(y) and the kernel first forms dy (written to dyo if set): g * act'(y)
@@ -198,8 +208,13 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
   constexpr int NT = bwd_threads<TPR, NV, LSUM, ACT>();
   constexpr int GPB = NT / TPR;
   constexpr int ROWF = TPR * NV * 4;  // floats a group covers
+  constexpr bool SPLIT = LSUM && is_softmax_act(ACT);
   __shared__ float lds[2 * (NT / 64)];
-  __shared__ float comb[GPB > 1 ? GPB * ROWF : 1];
+  // the softmax positional-sum split combines its groups in the dynamic LDS
+  // (lsum_dyn_bytes), which first stages each position's dx rows
+  __shared__ float comb_static[(GPB > 1 && !SPLIT) ? GPB * ROWF : 1];
+  extern __shared__ __align__(16) float dyn_lds[];
+  float* comb = SPLIT ? dyn_lds : comb_static;
   const int t = threadIdx.x % TPR;
   const int gi = threadIdx.x / TPR;
   const int h4 = H >> 2;
@@ -398,15 +413,30 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
     // as the node-by-node kernels do, so dx has their bits) and writes dx.
     // After a barrier the block's threads take the row's columns, and each
     // adds its column over the position's rows in batch order, starting from
-    // 0.0f, re-reading dx (just written by this CU: from L2): the sequential
-    // sum oxi_reduce(SUM) forms over the leading dim, bit for bit. One wave
-    // per position walking all its rows (below) runs this VJP at one wave
-    // per SIMD: 42-44 us at C5's (16, 1024, 768); split, 4 waves per SIMD at
-    // 118 VGPRs: 39-41 us; the pass without the positional sum: 33 us.
+    // 0.0f: the sequential sum oxi_reduce(SUM) forms over the leading dim,
+    // bit for bit. The rows come from LDS, where each wave also put its dx
+    // rows, when the position fits there (lsum_staged; 48 KB at C5), else
+    // from dx again. One wave per position walking all its rows (below) runs
+    // this VJP at one wave per SIMD: 42-44 us at C5's (16, 1024, 768);
+    // split, re-reading dx through the caches (the x and g streams evict
+    // most of it from L2: 38% more HBM fetch than the pass needs): 39-41 us;
+    // staged in LDS: 36.6-36.9 us against 39.4 in the same runs; the pass
+    // without the positional sum: 33 us.
     const int lead = (int)(rows / T);
     const int q = (lead + GPB - 1) / GPB;  // rows of a position per wave
     const int b0 = gi * q;
     const int nb = max(0, min(lead, b0 + q) - b0);
+    // a position's dx rows fit the dynamic LDS: the column sums read them
+    // there (the same values, added in the same order)
+    const bool staged = lsum_staged(lead, H);
+    f4* const stage = reinterpret_cast<f4*>(dyn_lds);
+    auto stage_row = [&](const RowTile<TPR, NV>& dt, int bb) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int c = k * TPR + t;
+        if (c < h4) stage[(int64_t)bb * h4 + c] = dt.v[k];
+      }
+    };
     for (int64_t p = blockIdx.x; p < T; p += gridDim.x) {
       if (nb > 0) {
         // two rows in flight; every prefetch issues (past the wave's last row
@@ -417,29 +447,41 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
         for (int j = 0; j < nb; j += 2) {
           fetch(xb, gb, ib, mb, rj(j + 1));
           __builtin_amdgcn_sched_barrier(0);
-          process(xa, ga, ia, ma, rj(j));
+          process(xa, ga, ia, ma, rj(j));  // ga now holds the row's dx
+          if (staged) stage_row(ga, b0 + j);
           if (j + 1 >= nb) break;
           fetch(xa, ga, ia, ma, rj(j + 2));
           __builtin_amdgcn_sched_barrier(0);
           process(xb, gb, ib, mb, rj(j + 1));
+          if (staged) stage_row(gb, b0 + j + 1);
         }
       }
-      __syncthreads();  // every dx row of position p is written
-      for (int c = threadIdx.x; c < h4; c += NT) {
-        const f4* src = reinterpret_cast<const f4*>(dx + p * H) + c;
-        const int64_t step = T * (int64_t)h4;  // float4s from one batch row to the next
-        f4 acc = zero;
-        int bb = 0;
-        for (; bb + 4 <= lead; bb += 4) {
-          const f4 v0 = src[(int64_t)bb * step], v1 = src[(int64_t)(bb + 1) * step];
-          const f4 v2 = src[(int64_t)(bb + 2) * step], v3 = src[(int64_t)(bb + 3) * step];
-          acc = acc + v0;
-          acc = acc + v1;
-          acc = acc + v2;
-          acc = acc + v3;
+      __syncthreads();  // every dx row of position p is written (and staged)
+      if (staged) {
+        for (int c = threadIdx.x; c < h4; c += NT) {
+          const f4* src = stage + c;
+          f4 acc = zero;
+          for (int bb = 0; bb < lead; ++bb) acc = acc + src[(int64_t)bb * h4];
+          st_stream<NTS>(acc, reinterpret_cast<f4*>(lsum + p * H) + c);
         }
-        for (; bb < lead; ++bb) acc = acc + src[(int64_t)bb * step];
-        st_stream<NTS>(acc, reinterpret_cast<f4*>(lsum + p * H) + c);
+        __syncthreads();  // the next position's rows overwrite the stage
+      } else {
+        for (int c = threadIdx.x; c < h4; c += NT) {
+          const f4* src = reinterpret_cast<const f4*>(dx + p * H) + c;
+          const int64_t step = T * (int64_t)h4;  // float4s from one batch row to the next
+          f4 acc = zero;
+          int bb = 0;
+          for (; bb + 4 <= lead; bb += 4) {
+            const f4 v0 = src[(int64_t)bb * step], v1 = src[(int64_t)(bb + 1) * step];
+            const f4 v2 = src[(int64_t)(bb + 2) * step], v3 = src[(int64_t)(bb + 3) * step];
+            acc = acc + v0;
+            acc = acc + v1;
+            acc = acc + v2;
+            acc = acc + v3;
+          }
+          for (; bb < lead; ++bb) acc = acc + src[(int64_t)bb * step];
+          st_stream<NTS>(acc, reinterpret_cast<f4*>(lsum + p * H) + c);
+        }
       }
     }
   } else if constexpr (LSUM) {
@@ -702,6 +744,17 @@ int launch_fwd(const float* x, const float* w, const float* b, float* y, float* 
   return check_launch(LN ? "layer_norm_fwd" : "rms_norm_fwd");
 }
 
+// Dynamic LDS of a lead-sum launch: for the softmax split, its group combine
+// (4 groups x 64 lanes x NV float4s) or, when staged, the position's dx rows
+// if larger; nothing for the walk.
+template <int NV, int ACT>
+size_t lsum_dyn_bytes(int64_t lead, int64_t H) {
+  if (!is_softmax_act(ACT)) return 0;
+  const size_t comb = sizeof(float) * (size_t)(LSUM_SPLIT_THREADS / 64) * (64 * NV * 4);
+  const size_t stage = lsum_staged(lead, H) ? sizeof(float) * (size_t)(lead * H) : 0;
+  return std::max(comb, stage);
+}
+
 template <bool LN, int MODE, bool NTS, int ACT>
 void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x, const float* w, const float* b,
                     const float* mean, const float* rstd, const float* g, float* dyo, float* dx, float* part,
@@ -713,7 +766,8 @@ void launch_bwd_cfg(int cfg, hipStream_t s, int64_t nblk, int nt, const float* x
     break;
 #define OXI_BWD_LSUM(NV)                                                                                   \
   case 640 + NV:                                                                                           \
-    norm_bwd_k<64, NV, MODE, LN, NTS, ACT, true><<<dim3((unsigned)nblk), dim3(bwd_threads<64, NV, true, ACT>()), 0, s>>>( \
+    norm_bwd_k<64, NV, MODE, LN, NTS, ACT, true><<<dim3((unsigned)nblk), dim3(bwd_threads<64, NV, true, ACT>()), \
+                                                   lsum_dyn_bytes<NV, ACT>(rows / T, h), s>>>(              \
         x, w, b, mean, rstd, g, dyo, dx, part, rows, h, lsum, T);                                          \
     break;
   if (lsum) {  // one-wave rows only (lsum_check)
