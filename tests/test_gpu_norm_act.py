@@ -382,10 +382,11 @@ def test_graph_fusion_x_grad_only_and_exact_mode(ox, vjp):
 
 # (4, 2500, 768) and (4, 1500, 512): more positions than the softmax split's
 # blocks, so its blocks take several positions each. A position's dx rows
-# are staged in LDS up to 56 KB: (32, 40, 512) and (32, 1100, 512), 64 KB,
-# re-read dx instead, the second with several positions per block
+# are staged in LDS up to 56 KB ((28, 50, 512) stages exactly 56 KB): (32,
+# 40, 512) and (32, 1100, 512), 64 KB, re-read dx instead, the second with
+# several positions per block
 LEAD_SHAPES = [(16, 1024, 768), (4, 300, 256), (8, 64, 1024), (4, 7, 36), (12, 5, 768), (16, 3, 64), (32, 40, 512),
-               (4, 2500, 768), (4, 1500, 512), (32, 1100, 512)]
+               (4, 2500, 768), (4, 1500, 512), (32, 1100, 512), (28, 50, 512)]
 
 
 @pytest.mark.parametrize("act", ["none", "silu", "gelu_erf", "softmax"])
