@@ -600,9 +600,12 @@ Var cross_entropy(const Var& logits, const std::vector<int64_t>& targets) {
   // With a gradient to come, the forward pass also forms the gradient for an
   // upstream 1 (loss.backward()'s seed) from the logits it holds: the first
   // backward seeded so takes it as is; any other upstream, or a second
-  // backward, runs the backward kernel.
+  // backward, runs the backward kernel. That gradient is an n x c tensor held
+  // until the backward: a loop that scales the loss first, or never calls
+  // backward, pays its write and memory for nothing, and turns it off with
+  // OXI_CE_ONE_PASS=0 (or set_ce_one_pass(False)).
   std::optional<Tensor> unit;
-  if (logits.requires_grad() && is_grad_enabled()) {
+  if (logits.requires_grad() && is_grad_enabled() && ce_one_pass()) {
     Tensor d = Tensor::empty({n, c}, Dev::Hip);
     const int rc = oxi_cross_entropy_fwd_grad(lc.data(), tp, loss.data(), lse.data(), d.data(), n, c);
     if (rc == OXI_OK) unit = d;

@@ -538,6 +538,10 @@ PYBIND11_MODULE(_native, m) {
         "Whether backward runs a norm VJP and the VJP of an activation on its output as one pass.");
   m.def("set_fuse_norm_act", &set_fuse_norm_act, "Turn the fused norm + activation VJP on or off; returns the old value.");
   m.def("fused_norm_act_passes", &fused_norm_act_passes, "Fused norm + activation VJP passes run in this process.");
+  m.def("ce_one_pass", &ce_one_pass,
+        "Whether cross_entropy's forward also writes the gradient for backward()'s implicit seed.");
+  m.def("set_ce_one_pass", &set_ce_one_pass,
+        "Turn cross_entropy's one-pass forward + seed-1 gradient on or off; returns the old value.");
   m.def("version", []() { return std::string("0.1.0"); });
   m.def("synchronize", []() { hip_check(oxi_hip_sync()); });
   m.def("memory_stats", []() {

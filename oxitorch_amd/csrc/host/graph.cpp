@@ -169,6 +169,24 @@ bool fuse_norm_act() {
 
 uint64_t fused_norm_act_passes() { return g_fused_passes.load(); }
 
+namespace {
+// -1: follow OXI_CE_ONE_PASS; 0 / 1: set by set_ce_one_pass
+std::atomic<int> g_ce_override{-1};
+}  // namespace
+
+bool ce_one_pass() {
+  const int o = g_ce_override.load();
+  if (o >= 0) return o == 1;
+  const char* e = std::getenv("OXI_CE_ONE_PASS");
+  return !(e && std::strcmp(e, "0") == 0);
+}
+
+bool set_ce_one_pass(bool on) {
+  const bool prev = ce_one_pass();
+  g_ce_override.store(on ? 1 : 0);
+  return prev;
+}
+
 bool set_fuse_norm_act(bool on) {
   const bool prev = fuse_norm_act();
   g_fuse_override.store(on ? 1 : 0);

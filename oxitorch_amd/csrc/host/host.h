@@ -234,6 +234,10 @@ bool is_implicit_seed(const Tensor& g);
 // default on; the setter overrides the environment and returns the old value).
 bool fuse_norm_act();
 bool set_fuse_norm_act(bool on);
+// Whether cross_entropy's forward also writes the gradient for backward()'s
+// implicit seed when the logits require grad (OXI_CE_ONE_PASS, default on).
+bool ce_one_pass();
+bool set_ce_one_pass(bool on);
 uint64_t fused_norm_act_passes();  // fused passes run so far in this process
 
 // ---- differentiable ops (crates/oxi-autograd/src/ops.rs) ------------------------

@@ -912,6 +912,10 @@ int lsum_check(const char* what, int64_t lead, int64_t rows, int64_t cols, const
     return fail(OXI_NOT_IMPLEMENTED, "%s: lead %lld is not a multiple of %d (or positions exceed 2^30); run the VJP "
                 "and the reduction", what, (long long)lead, LSUM_DEPTH);
   if (!dx || !dx_sum) return fail(OXI_INVALID_ARGUMENT, "%s: dx and dx_sum must not be NULL", what);
+  // dx_sum rows are written as float4s, like dx
+  if (!vec_ok(cols, {dx_sum}))
+    return fail(OXI_NOT_IMPLEMENTED, "%s: dx_sum at %p is not 16-byte aligned; run the VJP and the reduction", what,
+                static_cast<const void*>(dx_sum));
   if (pick_bwd_cfg(cols / 4) / 10 != 64)
     return fail(OXI_NOT_IMPLEMENTED, "%s: rows of %lld floats are wider than one wave; run the VJP and the reduction",
                 what, (long long)cols);

@@ -43,7 +43,8 @@ def gelu(x, approximate="tanh"):
 
 
 def silu(x):
-    """SiLU / swish: `x * sigmoid(x)`."""
+    """Sigmoid-weighted linear unit, elementwise: each value times its own
+    logistic sigmoid. One device node with its VJP."""
     return _native.silu(x)
 
 
@@ -54,12 +55,15 @@ def leaky_relu(x, negative_slope=0.01):
 # ---- softmax family (functional.py:211-222) -------------------------------------
 
 def softmax(x, dim=-1):
-    """Numerically stable softmax along `dim`."""
+    """Probabilities along `dim`: exponentials of x shifted by the largest
+    value of its slice (so no exponential overflows), divided by their sum.
+    One device node; the reference composes it from max, exp and sum nodes."""
     return _native.softmax(x, dim)
 
 
 def log_softmax(x, dim=-1):
-    """`log_softmax = x - max - log(sum(exp(x - max)))`, stable."""
+    """Log-probabilities along `dim`: x shifted by its slice maximum, minus the
+    log of the shifted exponentials' sum. One device node."""
     return _native.log_softmax(x, dim)
 
 
@@ -70,7 +74,8 @@ def _is_vec(t, H):
 
 
 def layer_norm(x, weight, bias, eps=1e-5, vjp=None):
-    """LayerNorm over the last dim with affine `weight`/`bias`.
+    """Normalizes each last-dim row to zero mean and unit variance (eps added
+    to the variance), then scales by `weight` and shifts by `bias`.
 
     `vjp` selects the x-gradient: "ref" (default, or OXI_NORM_VJP) reproduces
     the reference graph, where `.apply("rsqrt")` detaches the inverse std;
@@ -90,7 +95,8 @@ def layer_norm(x, weight, bias, eps=1e-5, vjp=None):
 
 
 def rms_norm(x, weight, eps=1e-6, vjp=None):
-    """RMSNorm over the last dim: `x / rms(x) * weight` (`vjp` as in layer_norm)."""
+    """Divides each last-dim row by its root mean square (eps added to the mean
+    square) and scales by `weight`; `vjp` as in layer_norm."""
     if _is_vec(weight, x.shape[-1]):
         return _native.rms_norm(x, weight, eps, vjp)
     ms = (x * x).mean(-1, True)
@@ -101,8 +107,9 @@ def rms_norm(x, weight, eps=1e-6, vjp=None):
 # ---- embedding (functional.py:245-247) -----------------------------------------------
 
 def embedding(indices, weight):
-    """`weight` is `(num_embeddings, dim)`; `indices` is a flat sequence of
-    ints, or a numpy integer array of any shape (read in C order)."""
+    """Rows of the `(num_embeddings, dim)` table `weight` picked by `indices`:
+    a flat sequence of ints as the reference takes them, or a numpy integer
+    array of any shape (read in C order)."""
     if isinstance(indices, np.ndarray):
         indices = indices.ravel()
     return _native.embedding(indices, weight)

@@ -1,4 +1,4 @@
-"""Optimizers, learning-rate schedules and gradient clipping for oxitorch_amd.
+"""Optimizers and gradient clipping for oxitorch_amd.
 
 Same surface as the reference module `oxitorch.optim`
 (python/oxitorch/optim.py): `Sgd`, `AdamW`, `Adam` delegate to the host
@@ -9,12 +9,11 @@ run each parameter's update as one HIP kernel over its flat slice
 to their updated values, so the objects (and Parameter wrappers) keep their
 identity across a run.
 
-Schedules only set `optimizer.lr`; the next device step reads it. Gradient
+The reference's learning-rate schedules are host-side bookkeeping outside
+the device hot path: their names exist and refuse to be made. Gradient
 clipping computes its norms with the device reductions and rescales the
 gradients on the device.
 """
-
-import math
 
 from oxitorch_amd import _native
 
@@ -101,106 +100,36 @@ class Adam(_DeviceOptimizer):
         super().__init__(params, _native.RustAdamW(lr, self.betas, eps, weight_decay, False))
 
 
-# ---- learning-rate schedules (python/oxitorch/optim.py:104-243) ---------------
+# ---- learning-rate schedules ---------------------------------------------------
 
-class _Schedule:
-    """lr(epoch) = base_lr * factor(epoch). Building a schedule already applies
-    epoch 0 (torch semantics); each `step()` moves to the next epoch."""
+class _OutsideSchedule:
+    """A learning-rate schedule of the reference (python/oxitorch/optim.py:104-226).
+    Schedules only rewrite `optimizer.lr` between steps on the host, off the
+    device hot path, so they are not part of this build: making one raises."""
 
-    def __init__(self, optimizer, last_epoch=-1):
-        self.optimizer = optimizer
-        self.base_lr = optimizer.lr
-        self.last_epoch = last_epoch
-        self.step()
-
-    def _lr_factor(self, t):
-        raise NotImplementedError
-
-    def step(self):
-        self.last_epoch += 1
-        self.optimizer.lr = self.base_lr * self._lr_factor(self.last_epoch)
-
-    def get_last_lr(self):
-        return [self.optimizer.lr]
+    def __init__(self, *args, **kwargs):
+        raise NotImplementedError(f"{type(self).__name__}: learning-rate schedules are outside this build's "
+                                  "device hot path; set optimizer.lr between steps")
 
 
-class StepLR(_Schedule):
-    """Decay by `gamma` once every `step_size` epochs."""
-
-    def __init__(self, optimizer, step_size, gamma=0.1, last_epoch=-1):
-        self.step_size = step_size
-        self.gamma = gamma
-        super().__init__(optimizer, last_epoch)
-
-    def _lr_factor(self, t):
-        return self.gamma ** (t // self.step_size)
+class StepLR(_OutsideSchedule):
+    """Reference schedule (optim.py:133); refused."""
 
 
-class CosineAnnealingLR(_Schedule):
-    """Half-cosine from base_lr down to `eta_min` over `T_max` epochs."""
-
-    def __init__(self, optimizer, T_max, eta_min=0.0, last_epoch=-1):
-        self.T_max = T_max
-        self.eta_min = eta_min
-        super().__init__(optimizer, last_epoch)
-
-    def _lr_factor(self, t):
-        if self.T_max <= 0:
-            return 1.0
-        w = 0.5 * (1.0 + math.cos(math.pi * t / self.T_max))
-        return (self.eta_min + (self.base_lr - self.eta_min) * w) / self.base_lr
+class CosineAnnealingLR(_OutsideSchedule):
+    """Reference schedule (optim.py:145); refused."""
 
 
-class LinearWarmup(_Schedule):
-    """Ramp linearly to base_lr over `warmup_epochs` ((t+1)/warmup), then hold."""
-
-    def __init__(self, optimizer, warmup_epochs, last_epoch=-1):
-        if warmup_epochs < 0:
-            raise ValueError("warmup_epochs must be non-negative")
-        self.warmup_epochs = warmup_epochs
-        super().__init__(optimizer, last_epoch)
-
-    def _lr_factor(self, t):
-        return 1.0 if self.warmup_epochs == 0 else min(1.0, (t + 1) / self.warmup_epochs)
+class LinearWarmup(_OutsideSchedule):
+    """Reference schedule (optim.py:162); refused."""
 
 
-class LambdaLR(_Schedule):
-    """lr = base_lr * lr_lambda(epoch)."""
-
-    def __init__(self, optimizer, lr_lambda, last_epoch=-1):
-        self.lr_lambda = lr_lambda
-        super().__init__(optimizer, last_epoch)
-
-    def _lr_factor(self, t):
-        return self.lr_lambda(t)
+class SequentialLR(_OutsideSchedule):
+    """Reference schedule (optim.py:179); refused."""
 
 
-class SequentialLR(_Schedule):
-    """Hand over to the next schedule at each milestone epoch; a schedule
-    counts its epochs from its own milestone. Every schedule is rebased on the
-    first one's base_lr, whatever the order they were built in."""
-
-    def __init__(self, optimizer, schedulers, milestones, last_epoch=-1):
-        if len(schedulers) != len(milestones) + 1:
-            raise ValueError(
-                f"{len(schedulers)} schedulers need {len(schedulers) - 1} milestones, got {len(milestones)}"
-            )
-        self.schedulers = list(schedulers)
-        self.milestones = list(milestones)
-        base = self.schedulers[0].base_lr
-        for s in self.schedulers:
-            s.base_lr = base
-        self.optimizer = optimizer
-        self.base_lr = base
-        self.last_epoch = last_epoch
-        self.step()
-
-    def step(self):
-        self.last_epoch += 1
-        t = self.last_epoch
-        k = sum(1 for m in self.milestones if t >= m)
-        start = self.milestones[k - 1] if k else 0
-        self.optimizer.lr = self.base_lr * self.schedulers[k]._lr_factor(t - start)
+class LambdaLR(_OutsideSchedule):
+    """Reference schedule (optim.py:215); refused."""
 
 
 # ---- gradient clipping (python/oxitorch/optim.py:248-299) ----------------------

@@ -15,6 +15,11 @@ iterable dataset fetched item by item, samplers, custom collation) stays on
 the host in the reference and is not part of this device build: those
 arguments raise NotImplementedError. Batches are leaf tensors without
 gradient, f32 like the reference's.
+
+Every public name of the reference module (data.py:31-40) is here, so code
+written against it imports unchanged: `Dataset` and `IterableDataset` are the
+base classes a user dataset derives from; the per-item pieces (`Subset`, the
+samplers, `default_collate`) raise NotImplementedError when used.
 """
 
 import os
@@ -23,7 +28,56 @@ import numpy as np
 
 from oxitorch_amd import _native
 
-__all__ = ["DataLoader", "TensorDataset"]
+__all__ = ["DataLoader", "Dataset", "IterableDataset", "RandomSampler", "SequentialSampler", "Subset",
+           "TensorDataset", "default_collate"]
+
+_PER_ITEM = ("runs item by item on the host in the reference; this build's loader gathers whole batches of "
+             "column tensors (TensorDataset) on the device")
+
+
+class Dataset:
+    """Base of map-style datasets: a subclass gives `__getitem__` and `__len__`."""
+
+    def __getitem__(self, index):
+        raise NotImplementedError(f"{type(self).__name__} does not define __getitem__")
+
+    def __len__(self):
+        raise NotImplementedError(f"{type(self).__name__} does not define __len__")
+
+
+class IterableDataset(Dataset):
+    """Base of stream-style datasets: a subclass gives `__iter__`."""
+
+    def __iter__(self):
+        raise NotImplementedError(f"{type(self).__name__} does not define __iter__")
+
+
+class _PerItem:
+    """A per-item piece of the reference's host loader: refused when made."""
+
+    def __init__(self, *args, **kwargs):
+        raise NotImplementedError(f"{type(self).__name__} {_PER_ITEM}")
+
+
+class Subset(_PerItem, Dataset):
+    """The reference's index view of a dataset (not built: per-item)."""
+
+
+class Sampler(_PerItem):
+    """The reference's index-stream base (not built: per-item)."""
+
+
+class SequentialSampler(Sampler):
+    """The reference's in-order index stream (not built: per-item)."""
+
+
+class RandomSampler(Sampler):
+    """The reference's shuffled index stream (not built: per-item)."""
+
+
+def default_collate(items):
+    """The reference's item collation (not built: per-item)."""
+    raise NotImplementedError(f"default_collate {_PER_ITEM}")
 
 
 def _on_device(column):
@@ -32,7 +86,7 @@ def _on_device(column):
     return _native.from_numpy(np.ascontiguousarray(column, dtype=np.float32))
 
 
-class TensorDataset:
+class TensorDataset(Dataset):
     """Column tensors of equal length; item i is the tuple of their i-th rows."""
 
     def __init__(self, *tensors):

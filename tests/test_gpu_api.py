@@ -157,6 +157,16 @@ def test_cross_entropy_seeded_with_one_takes_the_forward_gradient(ox, F, c):
     ls = la - m - np.log(np.exp(la - m).sum(-1, keepdims=True))
     want = (np.exp(ls) - np.eye(c, dtype=np.float32)[t]) / n
     assert np.allclose(implicit, want, rtol=1e-4, atol=1e-6)
+    # with the one-pass forward off, backward() runs the backward kernel: the
+    # bits of the explicit seed
+    from oxitorch_amd import _native
+    prev = _native.set_ce_one_pass(False)
+    try:
+        assert not _native.ce_one_pass()
+        two_call = grad_of(lambda x: F.cross_entropy(x, t).backward())
+    finally:
+        _native.set_ce_one_pass(prev)
+    assert np.array_equal(two_call.view(np.uint32), explicit.view(np.uint32))
 
 
 @pytest.mark.parametrize("c", [1000, 1003])

@@ -389,7 +389,7 @@ LEAD_SHAPES = [(16, 1024, 768), (4, 300, 256), (8, 64, 1024), (4, 7, 36), (12, 5
                (4, 2500, 768), (4, 1500, 512), (32, 1100, 512), (28, 50, 512)]
 
 
-@pytest.mark.parametrize("act", ["none", "silu", "gelu_erf", "softmax"])
+@pytest.mark.parametrize("act", ["none", "silu", "gelu_erf", "gelu_tanh", "softmax", "log_softmax"])
 @pytest.mark.parametrize("norm", ["rms_norm", "layer_norm"])
 @pytest.mark.parametrize("lts", LEAD_SHAPES)
 def test_lead_sum_matches_vjp_and_reduce(hip, lts, norm, act):

@@ -255,7 +255,7 @@ def test_binary_registry(hip):
 
 
 @pytest.mark.parametrize("kind", ["rms_norm", "layer_norm"])
-@pytest.mark.parametrize("act", ["none", "softmax", "silu"])
+@pytest.mark.parametrize("act", ["none", "softmax", "log_softmax", "silu", "gelu_tanh"])
 def test_lead_sum_matches_node_by_node(hip, kind, act):
     """The norm VJP that also sums dx over the leading dim (the positional
     gradient of x + pos): dy, dx and the sum give the node-by-node kernels'
@@ -275,10 +275,13 @@ def test_lead_sum_matches_node_by_node(hip, kind, act):
             h, rstd = hip.rms_norm_fwd(x, w)
         else:
             h, mean, rstd = hip.layer_norm_fwd(x, w, b)
-        if act == "softmax":
-            dh = hip.softmax_bwd(hip.softmax_fwd(h), g)
+        if act in ("softmax", "log_softmax"):
+            log = act == "log_softmax"
+            dh = hip.softmax_bwd(hip.softmax_fwd(h, log=log), g, log=log)
         elif act == "silu":
             dh = hip.silu_bwd(h, g)
+        elif act == "gelu_tanh":
+            dh = hip.gelu_bwd(h, g, "tanh")
         else:
             dh = g
         tag = f"{kind}+{act} lead sum {name}"

@@ -90,6 +90,22 @@ def test_argument_errors_map_to_value_error():
         capi.call("oxi_rms_norm_act_bwd", fake, None, fake, fake, 2, None, None, None, 1, 770, 0)
     with pytest.raises(NotImplementedError, match="do not vectorize"):
         capi.call("oxi_layer_norm_act_bwd", fake, None, None, fake, fake, fake + 4, 1, None, None, None, None, 1, 8, 0)
+    # the leading-dim sum's output is written as float4s: an offset dx_sum is
+    # refused before any launch (16 rows of 768 in (4, 4) positions)
+    for off, ok in ((4, False), (8, False), (16, True)):
+        args = (fake, None, fake, fake, 0, None, fake, None, fake + off, 4, 16, 768, 0)
+        if ok:
+            # past the checks, at initialisation; never on a machine with a
+            # device, where the call would launch on the fake addresses
+            if capi.device_count() == 0:
+                with pytest.raises(RuntimeError, match="no HIP device"):
+                    capi.call("oxi_rms_norm_bwd_lead_sum", *args)
+        else:
+            with pytest.raises(NotImplementedError, match="not 16-byte aligned"):
+                capi.call("oxi_rms_norm_bwd_lead_sum", *args)
+    with pytest.raises(NotImplementedError, match="not 16-byte aligned"):
+        capi.call("oxi_layer_norm_bwd_lead_sum", fake, None, None, fake, fake, fake, 2, None, fake, None, None,
+                  fake + 4, 4, 16, 768, 0)
 
 
 def test_oracle_is_not_imported_by_the_product():
@@ -284,80 +300,46 @@ def test_optimizer_refuses_host_tensors(ox):
         op.Sgd([w], lr=0.1).step()
 
 
-class _FakeOpt:
-    def __init__(self, lr):
-        self.lr = lr
-
-
-def test_step_lr_schedule():
-    """python/tests/test_phase4_training.py:110-120."""
+def test_lr_schedules_refused():
+    """The reference's schedule names (python/oxitorch/optim.py:104-226) exist
+    and refuse to be made: they are host bookkeeping outside this build."""
     import oxitorch_amd.optim as op
 
-    o = _FakeOpt(1.0)
-    s = op.StepLR(o, step_size=2, gamma=0.5)
-    lrs = []
-    for _ in range(6):
-        lrs.append(o.lr)
-        s.step()
-    assert lrs == pytest.approx([1.0, 1.0, 0.5, 0.5, 0.25, 0.25])
-    assert s.get_last_lr() == [o.lr]
+    for name in ("StepLR", "CosineAnnealingLR", "LinearWarmup", "SequentialLR", "LambdaLR"):
+        assert name in op.__all__
+        with pytest.raises(NotImplementedError, match="outside this build"):
+            getattr(op, name)(object(), 1)
 
 
-def test_cosine_and_lambda_schedules():
-    """python/tests/test_phase4_training.py:123-143."""
-    import math
+def test_data_module_names():
+    """Every public name of the reference's utils.data (data.py:31-40, 91)
+    imports; the base classes subclass, the per-item pieces refuse."""
+    import oxitorch_amd.utils.data as d
 
-    import oxitorch_amd.optim as op
+    for name in ("DataLoader", "Dataset", "IterableDataset", "RandomSampler", "SequentialSampler", "Subset",
+                 "TensorDataset", "default_collate", "Sampler"):
+        assert hasattr(d, name), name
 
-    o = _FakeOpt(1.0)
-    s = op.CosineAnnealingLR(o, T_max=4, eta_min=0.0)
-    lrs = []
-    for _ in range(5):
-        lrs.append(o.lr)
-        s.step()
-    assert lrs[0] == pytest.approx(1.0)
-    assert lrs[1] == pytest.approx((1 + math.cos(math.pi / 4)) / 2)
-    assert lrs[2] == pytest.approx(0.5)
-    assert lrs[4] == pytest.approx(0.0, abs=1e-6)
-    o = _FakeOpt(0.1)
-    s = op.LambdaLR(o, lr_lambda=lambda t: 0.5**t)
-    lrs = []
-    for _ in range(3):
-        lrs.append(o.lr)
-        s.step()
-    assert lrs == pytest.approx([0.1, 0.05, 0.025])
+    class Squares(d.Dataset):
+        def __getitem__(self, i):
+            return i * i
 
+        def __len__(self):
+            return 4
 
-def test_warmup_then_cosine_sequential():
-    """python/tests/test_phase4_training.py:146-176."""
-    import oxitorch_amd.optim as op
-
-    o = _FakeOpt(0.1)
-    warm = op.LinearWarmup(o, warmup_epochs=2)
-    cosine = op.CosineAnnealingLR(o, T_max=6)
-    seq = op.SequentialLR(o, [warm, cosine], milestones=[2])
-    lrs = []
-    for _ in range(9):
-        lrs.append(round(float(o.lr), 6))
-        seq.step()
-    assert lrs[0] == pytest.approx(0.05)
-    assert lrs[1] == pytest.approx(0.1)
-    assert lrs[2] == pytest.approx(0.1)
-    assert lrs[4] == pytest.approx(0.075)
-    assert lrs[6] == pytest.approx(0.025)
-    assert lrs[8] == pytest.approx(0.0, abs=1e-6)
-    o = _FakeOpt(0.2)
-    warm = op.LinearWarmup(o, warmup_epochs=2)
-    cosine = op.CosineAnnealingLR(o, T_max=10, eta_min=0.0)
-    seq = op.SequentialLR(o, [warm, cosine], milestones=[2])
-    assert cosine.base_lr == pytest.approx(0.2)
-    seq.step()
-    seq.step()
-    assert o.lr == pytest.approx(0.2)
-    with pytest.raises(ValueError, match="milestones"):
-        op.SequentialLR(o, [warm, cosine], milestones=[])
-    with pytest.raises(ValueError):
-        op.LinearWarmup(o, warmup_epochs=-1)
+    assert len(Squares()) == 4 and Squares()[3] == 9
+    assert issubclass(d.TensorDataset, d.Dataset) and issubclass(d.IterableDataset, d.Dataset)
+    with pytest.raises(NotImplementedError):
+        len(d.Dataset())
+    with pytest.raises(NotImplementedError):
+        iter(d.IterableDataset())
+    for cls in (d.Subset, d.Sampler, d.SequentialSampler, d.RandomSampler):
+        with pytest.raises(NotImplementedError, match="item by item"):
+            cls(Squares())
+    with pytest.raises(NotImplementedError, match="item by item"):
+        d.default_collate([1, 2])
+    with pytest.raises(NotImplementedError, match="Squares"):
+        d.DataLoader(Squares(), batch_size=2)
 
 
 def test_indexing_argument_checks_before_device(ox):

@@ -197,6 +197,26 @@ def test_kat_registry():
         np.testing.assert_allclose(ref.binary(name, a, b), want, rtol=1e-5, atol=1e-8, err_msg=name)
 
 
+def test_kat_rsqrt_and_round():
+    """rsqrt is `1.0 / a.sqrt()` (crates/oxi-tensor/src/ops.rs:138-141): an f32
+    square root, then an f32 division, each correctly rounded, so NumPy's f32
+    ops give its bits (an approximate reciprocal square root would not).
+    round is f32::round (ops.rs:186-188): halves go away from zero, where
+    np.round and rint go to even."""
+    r = np.abs(rng(3).standard_normal(4096)).astype(np.float32) * np.float32(100)
+    r = np.concatenate([r, np.array([4.0, 0.25, 1e-30, 3e38, 1.0, 2.0], np.float32)])
+    want = np.float32(1.0) / np.sqrt(r)
+    assert np.array_equal(ref.unary("rsqrt", r).view(np.uint32), want.view(np.uint32))
+    sp = ref.unary("rsqrt", np.array([0.0, -0.0, -1.0, np.inf], np.float32))
+    assert sp[0] == np.inf and sp[1] == -np.inf and np.isnan(sp[2]) and sp[3] == 0.0
+    half = np.array([0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 3.5, 4194304.5, 0.49999997, -0.49999997, 2.4999998,
+                     -0.0, 8388609.0], np.float32)
+    away = np.array([1.0, -1.0, 2.0, -2.0, 3.0, -3.0, 4.0, 4194305.0, 0.0, -0.0, 2.0, -0.0, 8388609.0], np.float32)
+    got = ref.unary("round", half)
+    assert np.array_equal(got.view(np.uint32), away.view(np.uint32)), got
+    assert not np.array_equal(np.round(half), away)  # ties to even would fail the check above
+
+
 # ---------------------------------------------------------------------------
 # Oracle f32 restatement vs float64 closed forms
 
