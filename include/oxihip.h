@@ -100,6 +100,11 @@ int oxi_hip_init(int device);
 int oxi_hip_device_count(int* count);
 /* Index of the initialised device, or -1. */
 int oxi_hip_current_device(int* device);
+/* The device the library is bound to, or, before the first device use, the
+ * one it will bind: OXI_HIP_DEVICE (a device index) when set, else 0. Replaces
+ * the index of the reference's Device (crates/oxi-core/src/lib.rs:139-146),
+ * reported as "hip:N" by Tensor.device (bindings lib.rs:406-408). */
+int oxi_hip_default_device(int* device);
 /* Device storage: replaces the Arc<Vec<f32>> buffer (lib.rs:53-58). Blocks are
  * recycled by a stream-ordered caching allocator. `bytes == 0` yields NULL. */
 int oxi_hip_alloc(size_t bytes, void** out);

@@ -40,7 +40,7 @@ HIP_FLAGS = [
     f"-I{CSRC}",
 ]
 
-HIP_SOURCES = ["runtime.hip", "elementwise.hip", "norm.hip", "softmax.hip", "reduce.hip", "embedding.hip", "indexing.hip", "optim.hip", "transfer.hip"]
+HIP_SOURCES = ["runtime.hip", "elementwise.hip", "norm.hip", "norm_bwd_none.hip", "norm_bwd_gelu.hip", "norm_bwd_silu.hip", "norm_bwd_softmax.hip", "softmax.hip", "reduce.hip", "embedding.hip", "indexing.hip", "optim.hip", "transfer.hip"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -53,6 +53,7 @@ _SIGS = {
     "oxi_hip_init": [c_int],
     "oxi_hip_device_count": [ctypes.POINTER(c_int)],
     "oxi_hip_current_device": [ctypes.POINTER(c_int)],
+    "oxi_hip_default_device": [ctypes.POINTER(c_int)],
     "oxi_hip_alloc": [c_size, ctypes.POINTER(vp)],
     "oxi_hip_free": [vp],
     "oxi_hip_empty_cache": [],

@@ -25,12 +25,24 @@ struct PyTensor {
 
 PyTensor leaf(Tensor t, bool rg = false) { return PyTensor(Var::leaf(std::move(t), rg)); }
 
+// "cpu", or a HIP device: "hip" / "cuda" (the bound device, OXI_HIP_DEVICE
+// before the first device use) or "hip:N" / "cuda:N", which binds device N
+// (crates/oxi-core/src/lib.rs:139-146: a device is a family and an index).
+// The library runs on one device per process.
 Dev parse_device(const py::object& d) {
   if (d.is_none()) return default_device();
   const std::string s = py::str(d);
-  if (s == "cpu") return Dev::Cpu;
-  if (s == "hip" || s == "hip:0" || s == "cuda" || s == "cuda:0") return Dev::Hip;
-  err_invalid("unknown device \"" + s + "\" (expected \"cpu\" or \"hip\")");
+  if (s == "cpu" || s == "cpu:0") return Dev::Cpu;
+  const size_t colon = s.find(':');
+  const std::string fam = s.substr(0, colon);
+  if (fam != "hip" && fam != "cuda")
+    err_invalid("unknown device \"" + s + "\" (expected \"cpu\", \"hip\" or \"hip:N\")");
+  if (colon == std::string::npos) return Dev::Hip;
+  const std::string idx = s.substr(colon + 1);
+  if (idx.empty() || idx.size() > 6 || idx.find_first_not_of("0123456789") != std::string::npos)
+    err_invalid("invalid device index in \"" + s + "\"");
+  bind_device(std::stoi(idx));
+  return Dev::Hip;
 }
 
 // buffer_to_f32 (bindings lib.rs:31-42)
@@ -527,6 +539,8 @@ PYBIND11_MODULE(_native, m) {
         return leaf(from_buffer(array, parse_device(device)), requires_grad);
       },
       py::arg("array"), py::arg("requires_grad") = false, py::arg("device") = py::none());
+  m.def("current_device", []() { return hip_device_index(); },
+        "Index of the HIP device the library is bound to (or will bind at its first device use).");
   m.def("device_count", []() {
     int n = 0;
     hip_check(oxi_hip_device_count(&n));

@@ -64,6 +64,11 @@ enum class Dev { Cpu, Hip };
 Dev default_device();
 void set_default_device(Dev d);
 std::string dev_name(Dev d);
+// Binds the library to HIP device `index` at the first device use ("hip:N"):
+// ValueError past the visible devices or when another device is bound.
+void bind_device(int index);
+// The bound HIP device, or the one the first device use will bind.
+int hip_device_index();
 
 struct Storage {
   Dev dev;

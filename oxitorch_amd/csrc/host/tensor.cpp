@@ -115,7 +115,32 @@ Dev g_default = Dev::Hip;
 }
 Dev default_device() { return g_default; }
 void set_default_device(Dev d) { g_default = d; }
-std::string dev_name(Dev d) { return d == Dev::Cpu ? "cpu" : "hip:0"; }
+int hip_device_index() {
+  int d = 0;
+  hip_check(oxi_hip_default_device(&d));
+  return d;
+}
+
+std::string dev_name(Dev d) {
+  if (d == Dev::Cpu) return "cpu";
+  int i = 0;
+  return oxi_hip_default_device(&i) == OXI_OK ? "hip:" + std::to_string(i) : std::string("hip");
+}
+
+void bind_device(int index) {
+  int n = 0;
+  hip_check(oxi_hip_device_count(&n));
+  if (n > 0 && index >= n)
+    err_invalid("device index " + std::to_string(index) + " out of range for " + std::to_string(n) +
+                " HIP device(s)");
+  int cur = -1;
+  hip_check(oxi_hip_current_device(&cur));
+  if (cur >= 0 && cur != index)
+    err_invalid("this process runs on hip:" + std::to_string(cur) + " (one device per process); hip:" +
+                std::to_string(index) + " needs a process of its own, e.g. with OXI_HIP_DEVICE=" +
+                std::to_string(index));
+  if (cur < 0) hip_check(oxi_hip_init(index));
+}
 
 Storage::Storage(Dev d, size_t bytes) : dev(d), nbytes(bytes) {
   if (bytes == 0) return;

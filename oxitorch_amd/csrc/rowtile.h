@@ -51,7 +51,13 @@ __device__ __forceinline__ f4 exp4(const f4& v) { return f4{expf(v.x), expf(v.y)
 // 320 MB, non-temporal otherwise. Measured on MI355X (fwd+bwd steps): plain
 // stores gain 8% on a chain of 50 MB tensors and 1-3% on 268 MB ones, and
 // lose 16-35% on 0.5-1 GB outputs and ~10% on 12 MB ones.
-inline bool nt_stores(int64_t bytes) { return bytes < ((int64_t)32 << 20) || bytes > ((int64_t)320 << 20); }
+#ifndef OXI_NT_STORE_LO
+#define OXI_NT_STORE_LO (32 << 20)
+#endif
+#ifndef OXI_NT_STORE_HI
+#define OXI_NT_STORE_HI (320 << 20)
+#endif
+inline bool nt_stores(int64_t bytes) { return bytes < (int64_t)OXI_NT_STORE_LO || bytes > (int64_t)OXI_NT_STORE_HI; }
 
 // Threads per block of a row kernel whose rows take TPR threads: 256 (several
 // rows per block) when TPR divides 256, else one row per block of TPR.

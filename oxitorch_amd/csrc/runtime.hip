@@ -16,6 +16,8 @@
 #include <unordered_map>
 #include <vector>
 
+#include <cstdlib>
+
 #include "internal.h"
 
 namespace oxi {
@@ -140,11 +142,26 @@ void* noalloc_scratch() {
 
 std::mutex& noalloc_mutex() { return rt().scratch_mu; }
 
+// The device an implicit initialisation binds: OXI_HIP_DEVICE (a device
+// index), else 0; -1 with the error set when the variable is not an index.
+int env_device() {
+  const char* e = std::getenv("OXI_HIP_DEVICE");
+  if (!e || !*e) return 0;
+  char* end = nullptr;
+  const long v = std::strtol(e, &end, 10);
+  if (*end != '\0' || v < 0 || v > 1 << 20) {
+    fail(OXI_INVALID_ARGUMENT, "OXI_HIP_DEVICE=\"%s\" is not a device index", e);
+    return -1;
+  }
+  return (int)v;
+}
+
 bool ensure_init() {
   Runtime& r = rt();
   std::lock_guard<std::mutex> lk(r.mu);
   if (r.stream) return true;
-  return init_locked(r, 0) == OXI_OK;
+  const int dev = env_device();
+  return dev >= 0 && init_locked(r, dev) == OXI_OK;
 }
 
 hipStream_t stream() { return rt().stream; }
@@ -215,6 +232,15 @@ int oxi_hip_device_count(int* count) {
 int oxi_hip_current_device(int* device) {
   if (!device) return fail(OXI_INVALID_ARGUMENT, "device must not be NULL");
   *device = rt().device;
+  return OXI_OK;
+}
+
+int oxi_hip_default_device(int* device) {
+  if (!device) return fail(OXI_INVALID_ARGUMENT, "device must not be NULL");
+  const int bound = rt().device;
+  const int d = bound >= 0 ? bound : env_device();
+  if (d < 0) return OXI_INVALID_ARGUMENT;
+  *device = d;
   return OXI_OK;
 }
 

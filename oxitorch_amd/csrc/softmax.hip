@@ -61,9 +61,10 @@ __device__ __forceinline__ void group_online(Online& o, float* lds) {
 // ---------------------------------------------------------------------------
 // Last-dim kernels, register-resident rows.
 
-template <int TPR, int NV, bool LOG, bool NTS>
+template <int TPR, int NV, bool LOG, bool NTS, bool FULL>
 __global__ __launch_bounds__((row_block_threads(TPR))) void sm_fwd_k(const float* __restrict__ x, float* __restrict__ y,
-                                                                  int64_t rows, int H) {
+                                                                  int64_t rows, int H_arg) {
+  const int H = FULL ? 4 * TPR * NV : H_arg;  // FULL: rows of exactly TPR * NV float4s
   constexpr int NT = row_block_threads(TPR);
   constexpr int GPB = NT / TPR;
   __shared__ float lds[2 * (NT / 64)];
@@ -100,9 +101,10 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void sm_fwd_k(const float
   xt.template store<NTS>(y + row * H, h4, t);
 }
 
-template <int TPR, int NV, bool LOG, bool NTS>
+template <int TPR, int NV, bool LOG, bool NTS, bool FULL>
 __global__ __launch_bounds__((row_block_threads(TPR))) void sm_bwd_k(const float* __restrict__ y, const float* __restrict__ g,
-                                                                  float* __restrict__ dx, int64_t rows, int H) {
+                                                                  float* __restrict__ dx, int64_t rows, int H_arg) {
+  const int H = FULL ? 4 * TPR * NV : H_arg;  // FULL: rows of exactly TPR * NV float4s
   constexpr int NT = row_block_threads(TPR);
   constexpr int GPB = NT / TPR;
   __shared__ float lds[NT / 64];
@@ -467,12 +469,18 @@ int launch_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inn
     const int cfg = (len % 4 == 0 && aligned16({x, y})) ? pick_row_cfg(len / 4) : 0;
     const int h = (int)len;
     const bool nts = nt_stores(outer * len * 4);
-#define OXI_SMF(TPR, NV)                                                                                            \
-  case TPR * 10 + NV:                                                                                               \
-    if (nts) sm_fwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),         \
-                                           dim3(row_block_threads(TPR)), 0, s>>>(x, y, outer, h);                    \
-    else sm_fwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),            \
-                                         dim3(row_block_threads(TPR)), 0, s>>>(x, y, outer, h);                      \
+#define OXI_SMF_GO(TPR, NV, NTS, FULL)                                                                  \
+  sm_fwd_k<TPR, NV, LOG, NTS, FULL><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),         \
+                                     dim3(row_block_threads(TPR)), 0, s>>>(x, y, outer, h)
+#define OXI_SMF(TPR, NV)                                                                                   \
+  case TPR * 10 + NV:                                                                                      \
+    if (h == 4 * TPR * NV) {                                                                               \
+      if (nts) OXI_SMF_GO(TPR, NV, true, true);                                                            \
+      else OXI_SMF_GO(TPR, NV, false, true);                                                               \
+    } else {                                                                                               \
+      if (nts) OXI_SMF_GO(TPR, NV, true, false);                                                           \
+      else OXI_SMF_GO(TPR, NV, false, false);                                                              \
+    }                                                                                                      \
     break;
     switch (cfg) {
       OXI_SMF(64, 1)
@@ -486,6 +494,7 @@ int launch_fwd(const float* x, float* y, int64_t outer, int64_t len, int64_t inn
         sm_fwd_loop_k<LOG><<<dim3((unsigned)outer), dim3(BS), 0, s>>>(x, y, outer, h);
     }
 #undef OXI_SMF
+#undef OXI_SMF_GO
   } else {
     sm_fwd_col_k<LOG><<<dim3((unsigned)ceil_div(outer * inner, BS)), dim3(BS), 0, s>>>(x, y, outer, len, inner);
   }
@@ -499,12 +508,18 @@ int launch_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t
     const int cfg = (len % 4 == 0 && aligned16({y, g, dx})) ? pick_row_cfg(len / 4) : 0;
     const int h = (int)len;
     const bool nts = nt_stores(outer * len * 4);
-#define OXI_SMB(TPR, NV)                                                                                        \
-  case TPR * 10 + NV:                                                                                           \
-    if (nts) sm_bwd_k<TPR, NV, LOG, true><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),         \
-                                           dim3(row_block_threads(TPR)), 0, s>>>(y, g, dx, outer, h);                \
-    else sm_bwd_k<TPR, NV, LOG, false><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),            \
-                                         dim3(row_block_threads(TPR)), 0, s>>>(y, g, dx, outer, h);                  \
+#define OXI_SMB_GO(TPR, NV, NTS, FULL)                                                                  \
+  sm_bwd_k<TPR, NV, LOG, NTS, FULL><<<dim3((unsigned)ceil_div(outer, row_block_threads(TPR) / TPR)),         \
+                                     dim3(row_block_threads(TPR)), 0, s>>>(y, g, dx, outer, h)
+#define OXI_SMB(TPR, NV)                                                                                   \
+  case TPR * 10 + NV:                                                                                      \
+    if (h == 4 * TPR * NV) {                                                                               \
+      if (nts) OXI_SMB_GO(TPR, NV, true, true);                                                            \
+      else OXI_SMB_GO(TPR, NV, false, true);                                                               \
+    } else {                                                                                               \
+      if (nts) OXI_SMB_GO(TPR, NV, true, false);                                                           \
+      else OXI_SMB_GO(TPR, NV, false, false);                                                              \
+    }                                                                                                      \
     break;
     switch (cfg) {
       OXI_SMB(64, 1)
@@ -518,6 +533,7 @@ int launch_bwd(const float* y, const float* g, float* dx, int64_t outer, int64_t
         sm_bwd_loop_k<LOG><<<dim3((unsigned)outer), dim3(BS), 0, s>>>(y, g, dx, outer, h);
     }
 #undef OXI_SMB
+#undef OXI_SMB_GO
   } else {
     sm_bwd_col_k<LOG><<<dim3((unsigned)ceil_div(outer * inner, BS)), dim3(BS), 0, s>>>(y, g, dx, outer, len, inner);
   }

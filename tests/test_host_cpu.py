@@ -429,3 +429,40 @@ def test_out_of_scope_names_raise_not_implemented():
         with pytest.raises(NotImplementedError, match="outside this build's device hot path"):
             layer(4, 4)
     assert callable(nn.LeakyReLU)
+
+
+def test_device_strings(ox):
+    """A device is a family and an index (crates/oxi-core/src/lib.rs:139-146):
+    "cpu", "hip"/"cuda" or "hip:N"/"cuda:N"; anything else is a ValueError
+    before any device use."""
+    a = np.zeros(3, np.float32)
+    for bad in ("tpu", "hip:", "hip:x", "hip:-1", "cuda:1.5", "hip:0:0"):
+        with pytest.raises(ValueError, match="device"):
+            ox.from_numpy(a, device=bad)
+    assert ox.from_numpy(a, device="cpu").device == "cpu"
+
+
+def test_hip_device_env_is_checked():
+    """OXI_HIP_DEVICE names the device an implicit initialisation binds; a
+    value that is not an index is refused (in a child process: the variable is
+    read when the library first binds a device)."""
+    import os
+    import subprocess
+    import sys
+
+    code = ("import ctypes, sys\n"
+            "from oxitorch_amd import capi\n"
+            "d = ctypes.c_int(-7)\n"
+            "try:\n"
+            "    capi.call('oxi_hip_default_device', ctypes.byref(d))\n"
+            "except ValueError as e:\n"
+            "    print('ValueError', e)\n"
+            "else:\n"
+            "    print('device', d.value)\n")
+    env = dict(os.environ, PYTHONPATH=str(ROOT))
+    for val, want in (("abc", "ValueError"), ("-1", "ValueError"), ("3", "device 3"), ("", "device 0")):
+        env["OXI_HIP_DEVICE"] = val
+        out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+        assert want in out.stdout, (val, out.stdout, out.stderr)
+        if want == "ValueError":
+            assert "is not a device index" in out.stdout
