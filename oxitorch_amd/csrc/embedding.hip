@@ -16,10 +16,14 @@
 //      <= 64 positions, 64-vector column chunk) sums every run of equal keys
 //      in position order in f32 -- the reference's own order, so a run of at
 //      most one tile's length gives a bit-identical row -- writing it straight
-//      to the output; a longer run leaves per-tile partial sums; the same
+//      to the output (a run into the next tile too: its wave reads on); a
+//      longer run leaves per-tile partial sums formed in float64; the same
 //      launch writes the zero rows of keys that never occur;
 //   3. fix-up: each key of a longer run adds its partial sums in tile order in
-//      float64.
+//      float64, so its row is its float64 sum rounded once to f32 (the
+//      reference's sequential f32 sum drifts from that by up to a few hundred
+//      ulp over a 41k-position run; the parity bar for such rows is the
+//      float64 sum).
 // Every wave of step 2 does the same amount of work whatever the id
 // distribution (a key owning a third of all positions is spread over many
 // tiles).
@@ -406,8 +410,9 @@ __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict_
 //  * a run that starts in the tile and ends in the next one is finished by
 //    this wave, which reads on into the next tile's positions (the next tile's
 //    wave skips it);
-//  * a longer run (a "long key") is summed per tile into partial slots --
-//    2*tile+1 where it continues into the next tile, 2*tile where it ends --
+//  * a longer run (a "long key") is summed per tile in float64 into partial
+//    slots -- 2*tile+1 where it continues into the next tile, 2*tile where it
+//    ends --
 //    and the tile where it starts joins the owner list while the tile where it
 //    ends records itself in end_tile[key]; seg_fixup_k adds the slots.
 // Blocks past the segment work write zero rows for keys that never occur
@@ -421,7 +426,10 @@ __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict_
 #define OXI_SEG_U 8
 #endif
 constexpr int SEG_U = OXI_SEG_U;
-constexpr int ZR = 4;
+#ifndef OXI_SEG_ZR
+#define OXI_SEG_ZR 4
+#endif
+constexpr int ZR = OXI_SEG_ZR;  // zero rows per block
 // Waves per SIMD the segment kernel is held to: at 5 it fits 84 VGPRs with no
 // spill (unbounded, the compiler takes 120: 4 waves). Measured: C5's
 // embedding VJP 35.8-36.1 us against 38.5-38.8; C4's unchanged (145-148 us).
@@ -435,7 +443,7 @@ template <bool VEC, bool NTS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE))) void seg_wave_k(
     const float* __restrict__ g, int64_t outer, int64_t n, int64_t inner, int64_t len,
     const int* __restrict__ skeys, const int* __restrict__ perm, float* __restrict__ grad,
-    float* __restrict__ part, const int* __restrict__ present, int* __restrict__ owners,
+    double* __restrict__ part, const int* __restrict__ present, int* __restrict__ owners,
     int* __restrict__ owner_count, int* __restrict__ end_tile, int st, int64_t stiles, int chunks,
     int64_t seg_blocks) {
   using V = typename std::conditional<VEC, f4, float>::type;
@@ -501,9 +509,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE
   const int64_t u = (int64_t)chunk * 64 + lane;
   const bool active = u < units;
   const int64_t slot_head = 2 * tile, slot_tail = slot_head + 1;
+  constexpr int NC = VEC ? 4 : 1;
   for (int64_t o = 0; o < outer; ++o) {
     const float* gb = g + o * n * inner;
     V acc = V{};
+    // the same run summed in float64: what a partial slot of a long key
+    // (a run over more than two tiles) receives
+    double accd[NC];
+#pragma unroll
+    for (int q = 0; q < NC; ++q) accd[q] = 0.0;
     int start = first;
     for (int i = first; i < cnt; i += SEG_U) {
       V vals[SEG_U];
@@ -522,23 +536,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE
         const int q = i + j;
         if (q >= cnt) break;
         acc = acc + vals[j];
+        if constexpr (VEC) {
+          accd[0] += (double)vals[j].x;
+          accd[1] += (double)vals[j].y;
+          accd[2] += (double)vals[j].z;
+          accd[3] += (double)vals[j].w;
+        } else {
+          accd[0] += (double)vals[j];
+        }
         if (((ends >> q) & 1ull) && !(tail_ext && q == cnt - 1)) {  // run [start, q] ends here
           const int key = __builtin_amdgcn_readlane(my_key, q);
           if ((uint64_t)key < (uint64_t)len && active) {
             const bool to_tail = tail_inc && q == cnt - 1;
             const bool to_head = !to_tail && head_inc && start == 0;
-            float* dst;
-            if (to_tail || to_head) {  // partial slots are re-read by the fix-up: plain stores
-              dst = part + ((to_tail ? slot_tail : slot_head) * outer + o) * inner;
-              if constexpr (VEC) reinterpret_cast<f4*>(dst)[u] = acc;
-              else dst[u] = acc;
+            if (to_tail || to_head) {  // float64 partial slots, re-read by the fix-up: plain stores
+              double* dst = part + (((to_tail ? slot_tail : slot_head) * outer + o) * inner + u * NC);
+#pragma unroll
+              for (int c = 0; c < NC; ++c) dst[c] = accd[c];
             } else {
-              dst = grad + (o * len + key) * inner;
+              float* dst = grad + (o * len + key) * inner;
               if constexpr (VEC) st_stream<NTS>(acc, reinterpret_cast<f4*>(dst) + u);
               else st_stream<NTS>(acc, dst + u);
             }
           }
           acc = V{};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) accd[c] = 0.0;
           start = q + 1;
         }
       }
@@ -583,9 +606,8 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t n, int64_t inner, int64_t len, int st,
                                                    int64_t stiles, const int* __restrict__ skeys,
                                                    const int* __restrict__ owners, const int* __restrict__ owner_count,
-                                                   const int* __restrict__ end_tile, const float* __restrict__ part,
+                                                   const int* __restrict__ end_tile, const double* __restrict__ part,
                                                    float* __restrict__ grad, int c16, int* guard) {
-  using V = typename std::conditional<VEC, f4, float>::type;
   constexpr int NC = VEC ? 4 : 1;
   __shared__ double red[4][16][NC];
   const int64_t units = VEC ? inner / 4 : inner;
@@ -610,23 +632,20 @@ __global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t n, int
 #pragma unroll
       for (int q = 0; q < NC; ++q) a[q] = 0.0;
       for (int64_t j0 = sl; j0 < m; j0 += 16 * FXU) {
-        V v[FXU];
+        double v[FXU][NC];
 #pragma unroll
         for (int q = 0; q < FXU; ++q) {
           const int64_t j = min<int64_t>(j0 + 16 * q, m - 1);  // in range: loads issue together
           const int64_t slot = (j < m - 1) ? 2 * (ta + j) + 1 : 2 * tb;
-          v[q] = active ? reinterpret_cast<const V*>(part + (slot * outer + o) * inner)[u] : V{};
+          const double* src = part + ((slot * outer + o) * inner + u * NC);
+#pragma unroll
+          for (int c = 0; c < NC; ++c) v[q][c] = active ? src[c] : 0.0;
         }
 #pragma unroll
-        for (int q = 0; q < FXU; ++q) {
-          if (j0 + 16 * q < m) {
-            if constexpr (VEC) {
-              a[0] += v[q].x; a[1] += v[q].y; a[2] += v[q].z; a[3] += v[q].w;
-            } else {
-              a[0] += v[q];
-            }
-          }
-        }
+        for (int q = 0; q < FXU; ++q)
+          if (j0 + 16 * q < m)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) a[c] += v[q][c];
       }
       // lanes c, c+16, c+32, c+48 of a wave hold 4 slot lanes of column c
 #pragma unroll
@@ -771,7 +790,7 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   const int64_t stiles = ceil_div(n, st);
   // end tile per key and the owner list of long keys; partial rows
   Workspace wsi(((size_t)len + (size_t)stiles) * sizeof(int));
-  Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(float));
+  Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(double));
   if (!wsi.p || !wsp.p) return fail_alloc("index_select_bwd: apply workspace");
   int* end_tile = wsi.as<int>();
   int* owners = end_tile + len;
@@ -782,7 +801,7 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   if (p.applies++ > 0) {
     if (int rc = oxi_fill(reinterpret_cast<float*>(owner_count), 1, 0.0f)) return rc;  // 0.0f is all-zero bits
   }
-  float* part = wsp.as<float>();
+  double* part = wsp.as<double>();
   const int64_t seg_blocks = ceil_div(stiles * chunks, 4);
   // the rows of g stream through the cache while dW is written: decide on
   // the launch's whole traffic, not on dW alone

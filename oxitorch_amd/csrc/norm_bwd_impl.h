@@ -33,7 +33,7 @@ __device__ __forceinline__ float rsum1(float v, float* lds) { return group_sum_o
 #define OXI_LSUM_SPLIT_THREADS 256
 #endif
 #ifndef OXI_LSUM_SPLIT_NT
-#define OXI_LSUM_SPLIT_NT 0
+#define OXI_LSUM_SPLIT_NT 1
 #endif
 constexpr int LSUM_SPLIT_THREADS = OXI_LSUM_SPLIT_THREADS;  // a position's waves with a softmax
 template <int TPR, int NV, bool LSUM = false, int ACT = OXI_ACT_NONE>
@@ -194,8 +194,7 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
 #pragma unroll
         for (int k = 0; k < NV; ++k) pk[k] = pk[k] - L;
       } else {
-#pragma unroll
-        for (int k = 0; k < NV; ++k) pk[k] = pk[k] / s;
+        div_by_sum<NV>(pk, s);  // e / s, rounded as the division operator rounds it
       }
       float sg = 0.f;
 #pragma unroll

@@ -45,7 +45,55 @@ constexpr float NEG_INF = -__builtin_huge_valf();
 __device__ __forceinline__ float max4(const f4& v) { return fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)); }
 __device__ __forceinline__ float min4(const f4& v) { return fminf(fminf(v.x, v.y), fminf(v.z, v.w)); }
 __device__ __forceinline__ float sum4(const f4& v) { return (v.x + v.y) + (v.z + v.w); }
-__device__ __forceinline__ f4 exp4(const f4& v) { return f4{expf(v.x), expf(v.y), expf(v.z), expf(v.w)}; }
+// exp(z) for z <= 0 (and NaN), as the softmax family needs it (z = x - max,
+// or a log-probability): the steps of ROCm's expf -- a two-part product with
+// log2(e), exp2 of the reduced argument, an exponent scale, 0 below the log of
+// the smallest subnormal -- without its overflow select, which only acts for
+// z > 88.7. Two of its thirteen instructions fewer per element.
+__device__ __forceinline__ float exp_le0(float z) {
+  const float ph = z * 0x1.715476p+0f;                                      // z * log2(e), rounded
+  const float pl = fmaf(z, 0x1.4ae0bep-26f, fmaf(z, 0x1.715476p+0f, -ph));  // its residual + log2(e)'s low part
+  const float n = __builtin_rintf(ph);
+  const float r = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), (int)n);
+  return z < -0x1.9d1da0p+6f ? 0.0f : r;
+}
+__device__ __forceinline__ f4 exp4(const f4& v) { return f4{exp_le0(v.x), exp_le0(v.y), exp_le0(v.z), exp_le0(v.w)}; }
+
+// v[k] / s for the NV float4s of a row that share the sum s (the softmax's
+// exponentials, all >= 0), rounded to nearest like the division operator:
+// q = e * (1/s), then twice q + (e - q*s) * (1/s) with the remainder exact by
+// FMA, which lands on the rounded quotient whenever it is a normal number
+// (Markstein's correction; the first step brings q within an ulp). The
+// operator's own sequence recomputes the divisor's scaling and reciprocal for
+// every element: 11 instructions against these 5. A wave whose row could give
+// a subnormal quotient (an exponential in (0, 2^-100)) or whose sum is outside
+// [2^-20, 2^20] (NaN and inf included) divides with the operator.
+template <int NV>
+__device__ __forceinline__ void div_by_sum(f4 (&v)[NV], float s) {
+  // bits(e) - 1 >= bits(2^-100) - 1  <=>  e == 0 or e >= 2^-100 (for e >= 0)
+  unsigned lo = 0xffffffffu;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    lo = min(lo, __float_as_uint(v[k].x) - 1u);
+    lo = min(lo, __float_as_uint(v[k].y) - 1u);
+    lo = min(lo, __float_as_uint(v[k].z) - 1u);
+    lo = min(lo, __float_as_uint(v[k].w) - 1u);
+  }
+  const bool ok = lo >= __float_as_uint(0x1p-100f) - 1u && s >= 0x1p-20f && s <= 0x1p20f;
+  if (__all(ok)) {
+    const float rs = 1.0f / s;
+    auto q1 = [&](float e) {
+      float q = e * rs;
+      q = fmaf(fmaf(-q, s, e), rs, q);
+      return fmaf(fmaf(-q, s, e), rs, q);
+    };
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] = f4{q1(v[k].x), q1(v[k].y), q1(v[k].z), q1(v[k].w)};
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] = v[k] / s;
+  }
+}
 
 // Store hint for a launch writing `bytes` of output: plain between 32 MB and
 // 320 MB, non-temporal otherwise. Measured on MI355X (fwd+bwd steps): plain

@@ -95,8 +95,7 @@ __global__ __launch_bounds__((row_block_threads(TPR))) void sm_fwd_k(const float
 #pragma unroll
     for (int k = 0; k < NV; ++k) xt.v[k] = xt.v[k] - L;
   } else {
-#pragma unroll
-    for (int k = 0; k < NV; ++k) xt.v[k] = xt.v[k] / s;
+    div_by_sum<NV>(xt.v, s);  // e / s, rounded as the division operator rounds it
   }
   xt.template store<NTS>(y + row * H, h4, t);
 }

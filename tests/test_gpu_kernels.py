@@ -607,16 +607,29 @@ def test_embedding_c4_full(hip):
     np.testing.assert_array_equal(dW, dW2)  # deterministic, bitwise
     want32 = ref.index_select_bwd(g, (V, Dm), 0, ids)
     counts = np.bincount(ids, minlength=V)
-    one = segmented_runs_in_one_tile(ids, V)  # same position-order f32 sum as the reference
-    np.testing.assert_array_equal(dW[one], want32[one])
+    # at C4's size the VJP cuts the sorted positions into tiles of 64: a run
+    # within one tile or reaching into the next is summed by one wave in
+    # position order in f32, as the reference sums it (bit-exact); a longer
+    # run is summed in float64 and rounded once
+    one = segmented_runs_in_one_tile(ids, V, tile=64)
+    start = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    end = start + counts - 1
+    two = (counts > 0) & ~one & (end // 64 == start // 64 + 1)
+    short = one | two
+    np.testing.assert_array_equal(dW[short], want32[short])
     np.testing.assert_array_equal(dW[counts == 0], 0.0)
-    record("C4", "dW rows of one-tile runs (bit-exact)", {"n": int(dW[one].size), "worst_tol": 0.0, "arbitrated": 0})
-    heavy = np.flatnonzero(~one & (counts > 0))
+    record("C4", f"dW rows of runs within two tiles (bit-exact; {int(two.sum())} reach the next tile)",
+           {"n": int(dW[short].size), "worst_tol": 0.0, "arbitrated": 0})
+    heavy = np.flatnonzero((counts > 0) & ~short)
     exact = np.zeros((heavy.size, Dm))
     for j, v in enumerate(heavy):
         exact[j] = g[ids == v].astype(np.float64).sum(0)
-    record("C4", f"dW {heavy.size} multi-tile rows",
-           assert_reduction_close(dW[heavy], want32[heavy], exact, what="C4 heavy dW rows"))
+    # a float64 sum rounded once: within a tenth of the parity bar of the
+    # exact sum, no arbitration needed
+    np.testing.assert_allclose(dW[heavy], exact, rtol=1e-6, atol=1e-7)
+    stats = assert_reduction_close(dW[heavy], want32[heavy], exact, what="C4 heavy dW rows")
+    assert stats["arbitrated"] == 0
+    record("C4", f"dW {heavy.size} rows of runs over 3+ tiles (float64 sums)", stats)
     # conservation: sum over rows of dW equals the sum of all upstream rows
     assert np.allclose(dW.astype(np.float64).sum(0), g.astype(np.float64).sum(0), rtol=1e-5, atol=1e-3)
 
