@@ -156,6 +156,7 @@ void launch_fwd_cfg(int cfg, hipStream_t s, const float* x, const float* w, cons
     OXI_FWD(64, 4)
     OXI_FWD(256, 2)
     OXI_FWD(256, 4)
+    OXI_FWD(512, 2)
     OXI_FWD(256, 8)
     default:
       norm_fwd_loop_k<LN><<<dim3((unsigned)rows), dim3(BS), 0, s>>>(x, w, b, y, mean, rstd, rows, h, eps);
@@ -167,7 +168,10 @@ template <bool LN>
 int launch_fwd(const float* x, const float* w, const float* b, float* y, float* mean, float* rstd,
                int64_t rows, int64_t H, float eps) {
   hipStream_t s = stream();
-  const int cfg = vec_ok(H, {x, w, b, y}) ? pick_row_cfg(H / 4) : 0;
+  int cfg = vec_ok(H, {x, w, b, y}) ? pick_row_cfg(H / 4) : 0;
+#ifdef OXI_NORM_FWD_512X2
+  if (cfg == 2564) cfg = 5122;
+#endif
   const int h = (int)H;
   if (nt_stores(rows * H * 4)) launch_fwd_cfg<LN, true>(cfg, s, x, w, b, y, mean, rstd, rows, h, eps);
   else launch_fwd_cfg<LN, false>(cfg, s, x, w, b, y, mean, rstd, rows, h, eps);

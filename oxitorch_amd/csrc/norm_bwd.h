@@ -86,9 +86,15 @@ inline int pick_bwd_cfg(int64_t h4) {
 #endif
 // Blocks per CU of a backward launch of nt-thread blocks that writes column
 // partials (the softmax positional-sum split aside); the partial buffer's
-// size and the launch both come from it. (measured: 2 blocks per CU beat 3
-// and 4 for 4096-float rows)
-constexpr int bwd_blocks_per_cu(int nt) { return nt == 1024 ? OXI_BWD_BPC1024 : 2; }
+// size and the launch both come from it.
+// Blocks per CU of the other (512- and 256-thread) backward blocks: 1 took
+// C2's layer_norm + erf-GELU VJP from 156.7 to 138.3 us in the warm step
+// (half the column partials, and their finish, at the same bandwidth);
+// 3 measured 156.0.
+#ifndef OXI_BWD_BPC_OTHER
+#define OXI_BWD_BPC_OTHER 1
+#endif
+constexpr int bwd_blocks_per_cu(int nt) { return nt == 1024 ? OXI_BWD_BPC1024 : OXI_BWD_BPC_OTHER; }
 
 // Bytes of column partials the backward needs for (rows, H): 2 x blocks x H
 // floats, or 0 when neither dw nor db is wanted.

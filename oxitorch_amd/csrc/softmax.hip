@@ -299,23 +299,33 @@ __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logi
 // Measured at C3 (8192 x 32000), two-exp form: 512 x 16 ran the forward with
 // the gradient in 380 us (1024 x 8, held to one block per CU by its 68 VGPRs:
 // 476 us; 256 x 32: 417 us) and the forward alone in 181 us (streaming: 174 us).
-template <int RT, int NV, bool GRAD, bool NTS>
+// TAIL1: the row fills all but the last of a thread's NV float4 slots
+// ((NV - 1) * RT < C / 4 <= NV * RT, as at C3's 32000 classes), so only slot
+// NV - 1 is bounds-checked. The hot loops take the minimum over every logit;
+// the reference's NaN rule needs the minimum over the non-target ones, which
+// is formed again, with the target dropped, only for a row whose minimum
+// could make it NaN. The target's logit comes from the owning thread's
+// registers.
+template <int RT, int NV, bool GRAD, bool NTS, bool TAIL1>
 __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ logits,
                                                     const int64_t* __restrict__ targets, float* __restrict__ lse,
                                                     float* __restrict__ picked, float* __restrict__ dunit, int64_t n,
                                                     int C, int* __restrict__ guard) {
-  // slot sets: the max and the non-target minimum, then the sum
-  __shared__ float lds[3 * (RT / 64)];
+  // slot sets: the max and the minimum, then the sum, then the rare
+  // non-target minimum
+  __shared__ float lds[4 * (RT / 64)];
+  __shared__ float tlogit;
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x;
   const int c4 = C >> 2;
   const float* xr = logits + row * C;
   const f4* p = reinterpret_cast<const f4*>(xr);
+  auto in_row = [&](int k) { return (TAIL1 && k < NV - 1) || k * RT + t < c4; };
   f4 v[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int c = k * RT + t;
-    v[k] = c < c4 ? ld_stream(p + c) : f4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+    v[k] = in_row(k) ? ld_stream(p + c) : f4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
   }
   int64_t tg = targets[row];
   const bool bad = tg < 0 || tg >= C;
@@ -326,15 +336,30 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
   const bool own = ct - kt * RT == t;
   const int jt = (int)(tg & 3);
   float m = NEG_INF;
-  float mn = -NEG_INF;  // minimum over the non-target logits (onehot_nan)
+  float mn = -NEG_INF;  // minimum over the row's logits (padding lanes hold -inf: skipped)
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     m = fmaxf(m, max4(v[k]));
-    if (k * RT + t < c4) mn = fminf(mn, min4(k == kt && own ? drop_lane(v[k], jt) : v[k]));
+    if (in_row(k)) mn = fminf(mn, min4(v[k]));
+    if (k == kt) {
+      if (own) tlogit = jt == 0 ? v[k].x : jt == 1 ? v[k].y : jt == 2 ? v[k].z : v[k].w;
+    }
   }
   float nmn = -mn;
   group_max2_once<RT>(m, nmn, lds);
   const float ms = m == NEG_INF ? 0.f : m;
+  // the row can be NaN only if its minimum is: then the minimum without the
+  // target decides (block-uniform branch)
+  bool nan_row = onehot_nan(-nmn, m);
+  if (nan_row) {
+    float mt = -NEG_INF;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (in_row(k)) mt = fminf(mt, min4(k == kt && own ? drop_lane(v[k], jt) : v[k]));
+    float nmt = -mt;
+    nmt = group_max_once<RT>(nmt, lds + 3 * (RT / 64));
+    nan_row = onehot_nan(-nmt, m);
+  }
   // Lanes past the row hold -inf: their e is exp(-inf) = 0 and adds nothing.
   float s = 0.f;
 #pragma unroll
@@ -342,12 +367,13 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
     v[k] = exp4(v[k] - ms);
     s += sum4(v[k]);
   }
-  s = group_sum_once<RT, float>(s, lds + 2 * (RT / 64));
+  s = group_sum_once<RT, float>(s, lds + 2 * (RT / 64));  // its barrier also publishes tlogit
+  if constexpr (RT == 64) __syncthreads();                 // (one wave: no barrier in the reduction)
   const float L = logf(s);
   if (t == 0) {
     if (bad) atomicOr(guard, 1);
     lse[row] = m + L;
-    picked[row] = onehot_nan(-nmn, m) ? __builtin_nanf("") : (xr[tg] - m) - L;
+    picked[row] = nan_row ? __builtin_nanf("") : (tlogit - m) - L;
   }
   if constexpr (GRAD) {
     const float scale = 1.0f / (float)n;
@@ -356,13 +382,15 @@ __global__ __launch_bounds__(RT) void ce_fwd_rows_k(const float* __restrict__ lo
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int c = k * RT + t;
-      if (c < c4) {
+      if (in_row(k)) {
         f4 d = v[k] * gs;
-        if (k == kt && own) {
-          if (jt == 0) d.x -= scale;
-          else if (jt == 1) d.y -= scale;
-          else if (jt == 2) d.z -= scale;
-          else d.w -= scale;
+        if (k == kt) {
+          if (own) {
+            if (jt == 0) d.x -= scale;
+            else if (jt == 1) d.y -= scale;
+            else if (jt == 2) d.z -= scale;
+            else d.w -= scale;
+          }
         }
         st_stream<NTS>(d, q + c);
       }
@@ -609,17 +637,20 @@ int ce_forward(const char* what, const float* logits, const int64_t* targets, fl
   float* pk = picked.as<float>();
   const bool nt = nt_stores(n * c * 4);  // the gradient's stores
   switch (rt) {
+#define OXI_CE_GO(RT, GRAD, NTS, TAIL1)                                                                    \
+  ce_fwd_rows_k<RT, 16, GRAD, NTS, TAIL1><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, \
+                                                                          (int)c, guard_flag())
 #define OXI_CE_ROWS(RT)                                                                                     \
   case RT:                                                                                                  \
-    if (!dunit)                                                                                             \
-      ce_fwd_rows_k<RT, 16, false, false><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, nullptr, n, \
-                                                                           (int)c, guard_flag());           \
-    else if (nt)                                                                                            \
-      ce_fwd_rows_k<RT, 16, true, true><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, \
-                                                                         (int)c, guard_flag());             \
-    else                                                                                                    \
-      ce_fwd_rows_k<RT, 16, true, false><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, \
-                                                                          (int)c, guard_flag());            \
+    if (c4 > 15 * RT) {                                                                                     \
+      if (!dunit) OXI_CE_GO(RT, false, false, true);                                                        \
+      else if (nt) OXI_CE_GO(RT, true, true, true);                                                         \
+      else OXI_CE_GO(RT, true, false, true);                                                                \
+    } else {                                                                                                \
+      if (!dunit) OXI_CE_GO(RT, false, false, false);                                                       \
+      else if (nt) OXI_CE_GO(RT, true, true, false);                                                        \
+      else OXI_CE_GO(RT, true, false, false);                                                               \
+    }                                                                                                       \
     break;
     OXI_CE_ROWS(64)
     OXI_CE_ROWS(128)
@@ -627,6 +658,7 @@ int ce_forward(const char* what, const float* logits, const int64_t* targets, fl
     OXI_CE_ROWS(512)
     OXI_CE_ROWS(1024)
 #undef OXI_CE_ROWS
+#undef OXI_CE_GO
     default:
       ce_fwd_k<<<grid, dim3(CE_BS), 0, stream()>>>(logits, targets, lse, pk, n, (int)c, vec, guard_flag());
   }
