@@ -23,27 +23,35 @@ gradient (the host core forms it if its .grad is read); C3's forward also
 writes the gradient for loss.backward()'s seed 1, so its backward launches
 nothing.
 
-The main figure (`ms_per_step`, `value`) is the cold-MALL step: W untimed
-warmup steps, then exactly K steps, each preceded by an untimed 512 MiB fill
-(twice the 256 MB Infinity Cache) and timed alone with HIP events on the
-library stream (the stream every liboxihip kernel runs on); the median of
-the K. `gbs` (and `value`) divides the HBM bytes the step's kernels must move
-(each call's reads and writes; C4's gather counted as reading each distinct
-row of W once; checked against the PMC counters in
-profiles/pmc_traffic_<config>.md) by that time, against the 8 TB/s peak.
-`per_op_gbs` divides the metric's per-op algorithmic bytes (every F.* op
-reading its inputs and writing its outputs once) by the same time: the rate a
-step of separate ops would need, which passes the peak where the fused passes
-remove traffic. `warm` is the same step run back to back without fills.
+The main figure (`ms_per_step`, `value`) is the slower of two medians over
+K steps each (after W untimed warmup steps):
+- cold: every step is preceded by an untimed flush of a 512 MiB scratch buffer
+  (twice the 256 MB Infinity Cache), written and then read back, so the step
+  reads its inputs from HBM and the cache holds no dirty lines (`--flush
+  write` fills only, which leaves the fill's dirty lines for the step to write
+  back; `--flush read` only reads, which evicts nothing from the Infinity
+  Cache on this GPU and so behaves like the warm step);
+- warm: the steps back to back, each paying the write-back of the previous
+  step's outputs.
+Each step is timed alone with HIP events on the library stream (the stream
+every liboxihip kernel runs on). `gbs` (and `value`) divides the HBM bytes
+the step's kernels must move (each call's reads and writes; C4's gather
+counted as reading each distinct row of W once; checked against the PMC
+counters in profiles/pmc_traffic_<config>.md) by that time, against the
+8 TB/s peak. `per_op_gbs` divides the metric's per-op algorithmic bytes
+(every F.* op reading its inputs and writing its outputs once) by the same
+time: the rate a step of separate ops would need, which passes the peak where
+the fused passes remove traffic.
 
 Per config:
 - in_step_us: each C-ABI call's time inside the step, from HIP events around
-  every call of K more cold-MALL steps (median per call);
+  every call of K more steps under the graded protocol (median per call);
 - roofline: the dominant call (largest in-step time) against MI355X's 8 TB/s
   HBM peak, its in-step time from in_step_us; `traffic` is its HBM bytes per
   call from the committed rocprofv3 PMC summary
   profiles/pmc_traffic_<config>.md (FETCH_SIZE and WRITE_SIZE runs, scaled by
   a copy kernel's readings);
+- cold_after_fill_only_ms: cold steps after a write-only flush;
 - copy_floor_ms: the step's launch sequence with every call replaced by an
   identity copy moving the same number of bytes (warm): the practical floor
   for a step of that many launches and bytes on this GPU;
@@ -908,9 +916,10 @@ class Flush:
 
 
 def time_graded(hip, kernels, steps, flush, per_call):
-    """`steps` cold-MALL steps: each after an untimed fill, timed alone with
-    HIP events on the library stream. With per_call, events also sit between
-    the step's calls. Returns (step times in ms, {call: [ms per step]})."""
+    """`steps` steps, each after an untimed flush() (a no-op for warm steps),
+    timed alone with HIP events on the library stream. With per_call, events
+    also sit between the step's calls. Returns (step times in ms, {call: [ms
+    per step]})."""
     n = len(kernels)
     marks = (n + 1) if per_call else 2
     ev = Events(hip, steps * marks)
@@ -1135,9 +1144,9 @@ def _rate(nbytes, ms):
 def run_config(hip, key, args, flush):
     """Everything measured for one config; returns (compact block, detail).
 
-    The graded cold-MALL steps (W untimed warmup steps, then exactly K timed
-    steps) come first, then the in-step per-call steps, the warm step, and
-    the other measurements."""
+    W untimed warmup steps, then K cold and K warm timed steps (the graded
+    figure is the slower median), then K steps with per-call events under
+    the graded protocol, then the other measurements."""
     log(f"[{key}] building workload")
     wl = WORKLOADS[key](hip)
     kernels = wl.kernels()

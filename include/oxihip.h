@@ -240,10 +240,11 @@ int oxi_layer_norm_bwd(const float* x, const float* w, const float* mean, const 
  * memory: code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc. Same arguments and results as oxi_layer_norm_bwd (the
  * same kernels and launch shapes, so the outputs are bit-identical); the
- * column partials of dw/db (2 x blocks x cols floats, at most 2 x 2 x CUs x
- * cols) live in a fixed OXI_NOALLOC_SCRATCH_BYTES array in device memory
- * instead of a workspace: on a 256-CU MI355X that covers rows of up to 4096
- * floats. Larger sizes are refused with OXI_INVALID_ARGUMENT before anything
+ * column partials of dw/db (2 x blocks x cols floats, at most 2 x CUs x cols
+ * for rows wider than 768 floats) live in a fixed OXI_NOALLOC_SCRATCH_BYTES
+ * array in device memory instead of a workspace: on a 256-CU MI355X that
+ * covers rows of up to 8192 floats. Larger sizes are refused with
+ * OXI_INVALID_ARGUMENT before anything
  * is launched, and so is a call before oxi_hip_init (initialisation
  * allocates). Every call on one device shares the array and leaves it
  * holding its partials; nothing in it needs to start at zero. Calls from

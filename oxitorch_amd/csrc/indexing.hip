@@ -16,6 +16,9 @@
 // of x and the mask: each picked grid point takes the gradient of its rank.
 #include <cmath>
 
+#include <cstdlib>
+#include <cstring>
+
 #include "internal.h"
 #include "rowtile.h"
 
@@ -455,6 +458,202 @@ __global__ __launch_bounds__(MB) void msel_write_k(Grid<1> g, const float* __res
   }
 }
 
+// One pass over x and the mask: the record and the picks written at their
+// final offsets, so x crosses HBM once (the two passes above read it twice).
+// A block owns a chunk of MSEL_CHUNK consecutive tiles, taken from an atomic
+// ticket in the order blocks start, so a chunk only ever waits for chunks
+// whose blocks already run. It loads all its tiles, ranks each tile's picks,
+// publishes the chunk's pick count in status[chunk] (flag LB_AGG), then adds
+// the counts, or the inclusive prefix (flag LB_PRE), of the chunks before it,
+// walking back until it meets a prefix (a decoupled look-back; the first
+// wave reads 64 status words per poll), publishes its own inclusive prefix,
+// and stores each tile's picks through LDS as coalesced runs. The record and
+// the tile offsets keep the two-pass layout, so the VJP reads either.
+// Measured at (16384, 4096): one tile per block took 244 us against 178 us
+// for the two passes; without the ticket (block order) and without the walk
+// it took 87 us, with the ticket alone 213 us: 16384 device-scope adds on one
+// address serialise at about 8 ns each, and each walk holds its block's
+// registers while it waits. Chunks of 2, 4, 6 and 8 tiles: 198, 183, 212 and
+// 306 us (4 tiles: 84 VGPRs; 8: 160). Wider windows (the whole block's 256
+// words per poll) were slower. The status words carry the values, so relaxed
+// device-scope atomics order everything the walk needs. Every wait is
+// bounded: a walk that polls `spin_limit` times without progress (a negative
+// limit: at once) raises the guard flag (bit 4) and its chunk stores no
+// picks; the call reports a failed last chunk, oxi_hip_sync any other. The
+// output holds room for every grid point.
+constexpr uint64_t LB_AGG = 1ull << 62, LB_PRE = 2ull << 62, LB_VAL = (1ull << 62) - 1;
+#ifndef OXI_MSEL_CHUNK
+#define OXI_MSEL_CHUNK 4
+#endif
+constexpr int MSEL_CHUNK = OXI_MSEL_CHUNK;  // tiles per block of the one pass
+
+__device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// x values and pick bits of one thread's 4 grid elements (as pick_bits).
+template <bool FAST>
+__device__ __forceinline__ unsigned load_picks(const Grid<2>& g, const float* x, const float* m, int64_t e0,
+                                               int64_t E, float (&v)[4]) {
+  unsigned bits = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = 0.0f;
+  if (e0 >= E) return 0;
+  if constexpr (FAST) {
+    if (e0 + 4 <= E) {
+      const f4 xv = ld_stream(reinterpret_cast<const f4*>(x + e0));
+      const f4 mv = ld_stream(reinterpret_cast<const f4*>(m + e0));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = xv[k];
+        bits |= (unsigned)picked(xv[k], mv[k]) << k;
+      }
+      return bits;
+    }
+    for (int k = 0; k < 4 && e0 + k < E; ++k) {
+      v[k] = x[e0 + k];
+      bits |= (unsigned)picked(v[k], m[e0 + k]) << k;
+    }
+    return bits;
+  } else {
+    int64_t idx[MAXD], off[2];
+    grid_decode(g, e0, idx, off);
+    for (int k = 0; k < 4 && e0 + k < E; ++k) {
+      if (k) grid_step(g, idx, off);
+      v[k] = x[off[0]];
+      bits |= (unsigned)picked(v[k], m[off[1]]) << k;
+    }
+    return bits;
+  }
+}
+
+template <bool FAST, int CH>
+__global__ __launch_bounds__(MB) void msel_onepass_k(Grid<2> g, const float* __restrict__ x,
+                                                     const float* __restrict__ m, int64_t E, int64_t T,
+                                                     uint64_t* __restrict__ status, int* __restrict__ ticket,
+                                                     int64_t* __restrict__ offs, uint64_t* __restrict__ rec,
+                                                     float* __restrict__ out, int64_t* host_total, int* guard,
+                                                     int spin_limit) {
+  __shared__ uint64_t lds[CH][WAVES];
+  __shared__ float stage[TILE];
+  __shared__ int64_t s_chunk, s_pre;
+  if (threadIdx.x == 0) s_chunk = atomicAdd(ticket, 1);
+  __syncthreads();
+  const int64_t chunk = s_chunk;
+  const int64_t tile0 = chunk * CH;  // first tile of the chunk
+  const int lane = threadIdx.x & 63;
+  unsigned bits[CH][STEPS];
+  float v[CH][STEPS][4];
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j)
+      bits[c][j] = load_picks<FAST>(g, x, m, (tile0 + c) * TILE + (int64_t)j * MB * 4 + threadIdx.x * 4, E, v[c][j]);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    if (tile0 + c >= T) break;
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) {
+      uint64_t b[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) b[k] = __ballot((bits[c][j] >> k) & 1u);
+      if (lane < 4) {
+        uint64_t w = b[0];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) w = lane == k ? b[k] : w;
+        rec[(tile0 + c) * REC_WORDS + (j * WAVES + (threadIdx.x >> 6)) * 4 + lane] = w;
+      }
+    }
+  }
+  int rank[CH][STEPS], n[CH];
+  int N = 0;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    n[c] = step_ranks(bits[c], lds[c], rank[c]);  // the first barrier orders the ticket read
+    N += n[c];
+  }
+  if (threadIdx.x < 64) {  // the first wave walks back, 64 status words per poll
+    int64_t pre = 0;
+    bool ok = true;
+    if (chunk == 0) {
+      if (lane == 0) lb_store(status, LB_PRE | (uint64_t)N);
+    } else {
+      if (lane == 0) lb_store(status + chunk, LB_AGG | (uint64_t)N);
+      // Lane l reads status[hi - l]; chunks below 0 count as a prefix of 0.
+      // Chunk 0 publishes a prefix, so the walk ends by the window holding it.
+      for (int64_t hi = chunk - 1;; hi -= 64) {
+        const int64_t j = hi - lane;
+        uint64_t st = j >= 0 ? lb_load(status + j) : LB_PRE;
+        uint64_t need, pm;
+        for (int spins = 0;; ++spins) {
+          if (spin_limit < 0) {  // the host's switch that fails every wait
+            ok = false;
+            break;
+          }
+          // lanes up to the nearest prefix must have published
+          pm = __ballot((st >> 62) == 2);
+          need = pm ? (pm & (~pm + 1)) | ((pm & (~pm + 1)) - 1) : ~0ull;
+          if ((__ballot((st >> 62) == 0) & need) == 0) break;
+          if (spins >= spin_limit) {
+            ok = false;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          if ((st >> 62) == 0) st = lb_load(status + j);
+        }
+        if (!ok) break;
+        int64_t add = (need >> lane & 1) ? (int64_t)(st & LB_VAL) : 0;
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) add += __shfl_xor(add, s, 64);
+        pre += add;
+        if (pm) break;  // a prefix was in the window
+      }
+      if (ok && lane == 0) lb_store(status + chunk, LB_PRE | (uint64_t)(pre + N));
+    }
+    if (lane == 0) {
+      if (!ok) atomicOr(guard, 4);
+      s_pre = ok ? pre : -1;
+      int64_t o = pre;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        if (tile0 + c >= T) break;
+        offs[tile0 + c] = o;
+        o += n[c];
+        if (ok && tile0 + c == T - 1) {
+          offs[T] = o;
+          // system scope: the host polls it while the other blocks finish
+          __hip_atomic_store(host_total, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+      }
+    }
+  }
+  int64_t base = -1;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    if (c) __syncthreads();  // the previous tile's stage is read
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) {
+      int r = rank[c][j];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (bits[c][j] >> k & 1u) stage[r++] = v[c][j][k];
+    }
+    __syncthreads();
+    if (c == 0) base = s_pre;
+    if (base < 0) return;
+    float* o = out + base;
+#pragma unroll
+    for (int q = 0; q < TILE / MB; ++q) {
+      const int i = q * MB + threadIdx.x;
+      if (i < n[c]) o[i] = stage[i];
+    }
+    base += n[c];
+  }
+}
+
 // VJP: the grid point of pick rank r gets 0 + up[r] (the reference adds the
 // upstream gradient to a zero), every other point 0, stored at the point's
 // offset in `g` (stride set 0). A record whose total differs from `count`
@@ -575,6 +774,32 @@ int grid_size(const int64_t* shape, int ndim, int64_t* E, int64_t* T, const char
 
 int64_t record_bytes(int64_t T) { return 8 * (T + 1) + 8 * (int64_t)REC_WORDS * T; }
 
+// The one pass's pick total: the block of the last tile stores it to the
+// slot (system scope) before its own stores, and other blocks may still be
+// storing picks, so the host polls the slot instead of waiting for the
+// stream and returns while the kernel drains (the caller's next launches
+// queue behind it). The poll ends when the value arrives or the stream's
+// work has ended (then the slot holds the total, or -1 after a failed walk);
+// a failed stream returns its error.
+int poll_total(int64_t* slot, hipStream_t st, int64_t* total) {
+  for (unsigned i = 1;; ++i) {
+    const int64_t v = __atomic_load_n(slot, __ATOMIC_ACQUIRE);
+    if (v >= 0) {
+      *total = v;
+      return OXI_OK;
+    }
+    if ((i & 63) == 0) {  // a driver call now and then
+      const hipError_t e = hipStreamQuery(st);
+      if (e == hipSuccess) {
+        *total = __atomic_load_n(slot, __ATOMIC_ACQUIRE);
+        return OXI_OK;
+      }
+      if (e != hipErrorNotReady) return fail_hip(e, "hipStreamQuery(masked_select)");
+    }
+    __builtin_ia32_pause();
+  }
+}
+
 }  // namespace
 }  // namespace oxi
 
@@ -678,12 +903,67 @@ int oxi_masked_select(const float* x, const int64_t* x_strides, const float* mas
   const Grid<1> g1 = make_grid<1>(shape, ndim, st2);
   const bool fast2 = contiguous(g2, 0) && contiguous(g2, 1) && al16(x) && al16(mask);
   const bool fast1 = contiguous(g1, 0) && al16(x);
-  Workspace wc(sizeof(int) * (size_t)T);
   Workspace wr(record ? 0 : (size_t)record_bytes(T));
-  if (!wc.p || (!record && !wr.p)) return fail_alloc("masked_select: workspace");
+  if (!record && !wr.p) return fail_alloc("masked_select: workspace");
   int64_t* offs = static_cast<int64_t*>(record ? record : wr.p);
   uint64_t* rec = reinterpret_cast<uint64_t*>(offs + T + 1);
   hipStream_t st = stream();
+  // One pass when the output can hold every grid point (its tensor uses the
+  // first `count`), else the count pass, the scan and the write pass, which
+  // read x twice but allocate the output at its exact size: always with
+  // OXI_MASKED_SELECT_EXACT=1, for callers short of device memory.
+  const char* exact_env = std::getenv("OXI_MASKED_SELECT_EXACT");
+  const bool exact = exact_env && std::strcmp(exact_env, "1") == 0;
+  void* big = nullptr;
+  if (!exact && oxi_hip_alloc(sizeof(float) * (size_t)E, &big) == OXI_OK && big) {
+    const int64_t C = ceil_div(T, MSEL_CHUNK);
+    Workspace wl(sizeof(uint64_t) * (size_t)C + 16);  // chunk status words, then the ticket
+    if (!wl.p) {
+      oxi_hip_free(big);
+      return fail_alloc("masked_select: look-back workspace");
+    }
+    uint64_t* status = wl.as<uint64_t>();
+    int* ticket = reinterpret_cast<int*>(status + C);
+    // all-zero bits: no chunk published, ticket 0 (a fill kernel, not a memset)
+    if ((rc = oxi_fill(wl.as<float>(), 2 * C + 4, 0.0f)) != OXI_OK) {
+      oxi_hip_free(big);
+      return rc;
+    }
+    int64_t total = -1;
+    {
+      std::lock_guard<std::mutex> lk(readback_mutex());
+      int64_t* slot = readback_slot();
+      *static_cast<volatile int64_t*>(slot) = -1;
+      // polls of about 1 us: a wait past a second is a failure (never seen);
+      // OXI_MSEL_SPIN_LIMIT=-1 fails every wait, to test that path
+      const char* sl = std::getenv("OXI_MSEL_SPIN_LIMIT");
+      const int SPIN_LIMIT = sl && std::strcmp(sl, "-1") == 0 ? -1 : 1 << 20;
+      if (fast2)
+        msel_onepass_k<true, MSEL_CHUNK><<<(unsigned)C, MB, 0, st>>>(
+            g2, x, mask, E, T, status, ticket, offs, rec, static_cast<float*>(big), slot, guard_flag(), SPIN_LIMIT);
+      else
+        msel_onepass_k<false, MSEL_CHUNK><<<(unsigned)C, MB, 0, st>>>(
+            g2, x, mask, E, T, status, ticket, offs, rec, static_cast<float*>(big), slot, guard_flag(), SPIN_LIMIT);
+      if ((rc = check_launch("masked_select")) == OXI_OK) rc = poll_total(slot, st, &total);
+      if (rc != OXI_OK) {
+        oxi_hip_free(big);
+        return rc;
+      }
+    }
+    if (total < 0) {
+      oxi_hip_free(big);
+      return fail(OXI_OTHER, "masked_select: a tile's offset wait did not finish (look-back)");
+    }
+    if (total == 0) {
+      oxi_hip_free(big);
+      return OXI_OK;
+    }
+    *out = static_cast<float*>(big);
+    *count = total;
+    return OXI_OK;
+  }
+  Workspace wc(sizeof(int) * (size_t)T);
+  if (!wc.p) return fail_alloc("masked_select: workspace");
   if (fast2) msel_count_k<true><<<(unsigned)T, MB, 0, st>>>(g2, x, mask, E, wc.as<int>(), rec);
   else msel_count_k<false><<<(unsigned)T, MB, 0, st>>>(g2, x, mask, E, wc.as<int>(), rec);
   int64_t total = 0;

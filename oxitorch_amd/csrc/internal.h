@@ -50,9 +50,11 @@ void ws_free(void* p);
 // Device-side guard flag: kernels that meet an index outside its range set it;
 // oxi_hip_sync() reports it. Pointer to one int in device memory.
 int* guard_flag();
-// A pinned host int64 that a kernel can store one result to (a data-dependent
-// size, say), read by the host after the stream is synchronised: no copy call.
-// Callers hold readback_mutex() from the launch until the read.
+// A pinned, coherent host int64 that a kernel can store one result to (a
+// data-dependent size, say), read by the host after the stream is
+// synchronised, or polled while the kernel runs when the kernel stores it
+// with system scope: no copy call. Callers hold readback_mutex() from the
+// launch until the read.
 int64_t* readback_slot();
 std::mutex& readback_mutex();
 // Checks the launch that just happened.

@@ -84,13 +84,12 @@ inline int pick_bwd_cfg(int64_t h4) {
 #ifndef OXI_BWD_BPC1024
 #define OXI_BWD_BPC1024 1
 #endif
-// Blocks per CU of a backward launch of nt-thread blocks that writes column
-// partials (the softmax positional-sum split aside); the partial buffer's
-// size and the launch both come from it.
-// Blocks per CU of the other (512- and 256-thread) backward blocks: 1 took
-// C2's layer_norm + erf-GELU VJP from 156.7 to 138.3 us in the warm step
-// (half the column partials, and their finish, at the same bandwidth);
-// 3 measured 156.0.
+// Blocks per CU of the 512- and 256-thread backward blocks: 1 took C2's
+// layer_norm + erf-GELU VJP from 156.7 to 138.3 us in the warm step (half
+// the column partials, and their finish, at the same bandwidth); 2 was the
+// earlier setting, 3 measured 156.0. bwd_blocks_per_cu() sizes both the
+// launch and its column-partial buffer (the softmax positional-sum split
+// aside, which sizes its own).
 #ifndef OXI_BWD_BPC_OTHER
 #define OXI_BWD_BPC_OTHER 1
 #endif

@@ -26,9 +26,12 @@ __device__ __forceinline__ float rsum1(float v, float* lds) { return group_sum_o
 // wider rows 1 per block. The leading-sum walk (LSUM) runs 4 waves to a
 // block, each with LSUM_DEPTH rows in flight.
 // The softmax positional-sum split's block (waves per position) and whether
-// it loads x and g non-temporally. Measured at C5's (16, 1024, 768): 256
-// threads with plain loads 40.7 us; non-temporal loads 47.1 us; 512 and
-// 1024 threads (non-temporal) 47.4 and 52.0 us.
+// it loads x and g non-temporally. Measured at C5's (16, 1024, 768), in the
+// warm step: since the dx rows are staged in LDS (nothing re-read through
+// L2), non-temporal loads take 33-34 us against 44 us with plain ones, whose
+// lines evict the next kernels' inputs. Earlier, with dx re-read from L2,
+// 256 threads measured 40.7 us with plain loads and 47.1 us with
+// non-temporal ones, 512 and 1024 threads 47.4 and 52.0 us.
 #ifndef OXI_LSUM_SPLIT_THREADS
 #define OXI_LSUM_SPLIT_THREADS 256
 #endif

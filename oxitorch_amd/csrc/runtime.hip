@@ -92,7 +92,8 @@ int init_locked(Runtime& r, int device) {
   if ((e = hipMalloc(&r.guard, sizeof(int))) != hipSuccess) return fail_hip(e, "hipMalloc(guard)");
   if ((e = hipMemsetAsync(r.guard, 0, sizeof(int), r.stream)) != hipSuccess)
     return fail_hip(e, "hipMemsetAsync(guard)");
-  if ((e = hipHostMalloc(reinterpret_cast<void**>(&r.readback), sizeof(int64_t), hipHostMallocDefault)) != hipSuccess)
+  // coherent: a kernel's system-scope store reaches the host while it runs
+  if ((e = hipHostMalloc(reinterpret_cast<void**>(&r.readback), sizeof(int64_t), hipHostMallocCoherent)) != hipSuccess)
     return fail_hip(e, "hipHostMalloc(readback)");
   *r.readback = 0;
   if ((e = hipStreamSynchronize(r.stream)) != hipSuccess) return fail_hip(e, "hipStreamSynchronize");
@@ -354,7 +355,9 @@ int oxi_hip_sync(void) {
   if (flag != 0) {
     const int zero = 0;
     (void)hipMemcpy(guard_flag(), &zero, sizeof(int), hipMemcpyHostToDevice);
-    return fail(OXI_OUT_OF_BOUNDS, "a device kernel met an index outside its valid range; the affected output was written with zeros");
+    if (flag & 3)
+      return fail(OXI_OUT_OF_BOUNDS, "a device kernel met an index outside its valid range; the affected output was written with zeros");
+    return fail(OXI_OTHER, "masked_select: a tile's offset wait did not finish; that tile's picks were not written");
   }
   return OXI_OK;
 }

@@ -11,6 +11,7 @@ masked_select's count, record and output blocks; then the same for one whole
 forward + backward of the config-5 chain through the host core."""
 
 import gc
+import os
 import sys
 
 import numpy as np
@@ -165,10 +166,11 @@ def test_norm_vjp_workspace(hip, kind):
 
 
 def test_masked_select(hip):
-    """masked_select of a column broadcast over a 3-d mask: the per-tile
-    counts, the record (when the caller passes none) and the output block
-    each fail in turn; then the VJP's grid-order buffer, which the broadcast
-    x needs."""
+    """masked_select of a column broadcast over a 3-d mask. The record (when
+    the caller passes none) fails first. The one-pass path's output, sized for
+    every grid point, failing is not an error: the call takes the two-pass
+    path, whose per-tile counts and exact-size output then each fail in turn.
+    Then the VJP's grid-order buffer, which the broadcast x needs."""
     from oxitorch_amd.capi import DeviceArray
 
     r = rng(13)
@@ -184,7 +186,37 @@ def test_masked_select(hip):
     def recover():
         same_bits(hip.masked_select(x, mask).numpy(), clean, "masked_select")
 
-    made = sweep(hip, "masked_select", call, recover, "masked_select:")
+    # one pass: the record (1), the output for every grid point (2), the
+    # look-back status words (3). The output failing is not an error: the
+    # call takes the two-pass path, with the same bits.
+    base = hip.memory_stats()[0]
+    for k, site in ((1, "masked_select: workspace"), (2, None), (3, "masked_select: look-back workspace")):
+        say("masked_select one pass - allocation", k, "fails")
+        hip.lib.oxi_hip_debug_fail_alloc_after(k)
+        try:
+            got = hip.masked_select(x, mask)
+        except RuntimeError as e:
+            got, msg = None, str(e)
+        finally:
+            hip.lib.oxi_hip_debug_fail_alloc_after(0)
+        hip.sync()
+        if site is None:
+            assert got is not None, k
+            same_bits(got.numpy(), clean, "masked_select on the two-pass path")
+            got.free()
+        else:
+            assert got is None and INJECTED in msg and site in msg, (k, msg)
+        hip.sync()
+        assert hip.memory_stats()[0] == base, k
+        recover()
+    assert _attempt(hip, 4, call) is None  # no fourth allocation
+    # two passes (OXI_MASKED_SELECT_EXACT=1): the record, the per-tile counts
+    # and the exact-size output each fail in turn
+    os.environ["OXI_MASKED_SELECT_EXACT"] = "1"
+    try:
+        made = sweep(hip, "masked_select two-pass", call, recover, "masked_select:")
+    finally:
+        del os.environ["OXI_MASKED_SELECT_EXACT"]
     assert made == 3, made
 
     grid = tuple(np.broadcast_shapes(xs, ms))
@@ -204,6 +236,42 @@ def test_masked_select(hip):
 
     made = sweep(hip, "masked_select_bwd", bwd, bwd_recovers, "masked_select_bwd: workspace")
     assert made == 1, made
+
+
+def test_masked_select_offset_wait(hip):
+    """The one pass's offset wait failing, forced from the host: with
+    OXI_MSEL_SPIN_LIMIT=-1 every chunk but the first gives up its wait at
+    once (no kernel spins or faults). The call reports the failed last chunk,
+    returns every block it took, and oxi_hip_sync reports the guard; a grid of
+    one chunk never waits, and the next call gives the clean bits."""
+    from oxitorch_amd.capi import DeviceArray
+
+    r = rng(14)
+    shape = (64, 96, 128)  # 192 tiles of 4096 points: 48 chunks
+    xa = r.standard_normal(shape, dtype=np.float32)
+    ma = (r.random(shape) > 0.4).astype(np.float32)
+    x, mask = DeviceArray.from_numpy(xa), DeviceArray.from_numpy(ma)
+    clean = hip.masked_select(x, mask).numpy()
+    same_bits(clean, xa[ma != 0], "masked_select")
+    small_x = DeviceArray.from_numpy(xa[:1, :96, :128].copy())  # 12288 points: one chunk
+    small_m = DeviceArray.from_numpy(ma[:1, :96, :128].copy())
+    base = hip.memory_stats()[0]
+    say("masked_select one pass - every offset wait fails")
+    os.environ["OXI_MSEL_SPIN_LIMIT"] = "-1"
+    try:
+        with pytest.raises(RuntimeError, match="offset wait did not finish"):
+            hip.masked_select(x, mask)
+        with pytest.raises(RuntimeError, match="offset wait did not finish"):
+            hip.sync()
+        got = hip.masked_select(small_x, small_m)
+        same_bits(got.numpy(), xa[:1, :96, :128][ma[:1, :96, :128] != 0], "masked_select, one chunk")
+        got.free()
+        hip.sync()
+    finally:
+        del os.environ["OXI_MSEL_SPIN_LIMIT"]
+    assert hip.memory_stats()[0] == base
+    same_bits(hip.masked_select(x, mask).numpy(), clean, "masked_select after the failed waits")
+    hip.sync()
 
 
 def _c5_step(ox, F, data):

@@ -117,9 +117,20 @@ MASK_CASES = [((3, 4), (3, 4), 0.5), ((2, 1, 5), (3, 5), 0.6), ((4,), (3, 1), 0.
               ((1200000,), (1200000,), 0.0), ((1200000,), (1200000,), 0.00002), ((700, 3000), (700, 3000), 1.0)]
 
 
+@pytest.fixture(params=["one_pass", "two_pass"])
+def msel_path(request):
+    """The one-pass path (default: x read once, the output sized for every
+    grid point) and the two-pass path (OXI_MASKED_SELECT_EXACT=1)."""
+    import os
+    if request.param == "two_pass":
+        os.environ["OXI_MASKED_SELECT_EXACT"] = "1"
+    yield request.param
+    os.environ.pop("OXI_MASKED_SELECT_EXACT", None)
+
+
 @pytest.mark.parametrize("xs,ms,density", MASK_CASES)
-def test_masked_select_matches_oracle(hip, oracle, xs, ms, density):
-    say("masked_select", xs, ms, density)
+def test_masked_select_matches_oracle(hip, oracle, xs, ms, density, msel_path):
+    say("masked_select", msel_path, xs, ms, density)
     r = rng(20 + len(xs) * 7 + len(ms))
     x = r.standard_normal(xs, dtype=np.float32)
     m = (r.random(ms, dtype=np.float32) < density).astype(np.float32)
@@ -150,7 +161,7 @@ def test_masked_select_matches_oracle(hip, oracle, xs, ms, density):
     got.free()
 
 
-def test_masked_select_strided_operands(hip, oracle):
+def test_masked_select_strided_operands(hip, oracle, msel_path):
     """A transposed x and a broadcast column mask, through explicit strides."""
     say("masked_select strided")
     r = rng(5)

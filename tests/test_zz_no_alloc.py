@@ -83,11 +83,12 @@ def test_noalloc_partial_outputs_and_empty(hip):
 
 
 def test_noalloc_refuses_rows_beyond_the_scratch(hip):
-    """Rows of 8192 floats need 32 MiB of partials on a 256-CU device: refused
-    before any launch, with the limit in the message."""
+    """Rows of 12288 floats (past the register-row widths: one 256-thread
+    block per CU) need 2 x 256 x 12288 x 4 bytes (24 MiB) of partials on a
+    256-CU device: refused before any launch, with the limit in the message."""
     props = hip.device_props()
-    R, H = 2 * 2 * props["compute_units"], 8192
-    need = 2 * min(R, 2 * props["compute_units"]) * H * 4
+    R, H = 2 * 2 * props["compute_units"], 12288
+    need = 2 * min(R, props["compute_units"]) * H * 4
     assert need > hip.NOALLOC_SCRATCH_BYTES
     x = hip.DeviceArray((R, H))
     stats = hip.DeviceArray((R,))
