@@ -502,7 +502,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE
   const bool head_end = head_inc && !(tail_inc && single);
   const bool head_skip = head_end && key_prev2 != key0;
   if (chunk == 0 && lane == 0) {
-    if (tail_long && (uint64_t)keyl < (uint64_t)len) owners[atomicAdd(owner_count, 1)] = (int)tile;
+    if (tail_long && (uint64_t)keyl < (uint64_t)len) {
+      const int oi = atomicAdd(owner_count, 1);
+      owners[2 * oi] = (int)tile;  // with its key: one dependent load less in the fix-up
+      owners[2 * oi + 1] = keyl;
+    }
     if (head_end && !head_skip && (uint64_t)key0 < (uint64_t)len) end_tile[key0] = (int)tile;
   }
   const int first = head_skip ? __ffsll((long long)ends) : 0;  // one past the head run's end
@@ -600,6 +604,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE
 // (wave shuffles over the 4 slot lanes a wave holds, then the 4 waves in
 // order). Slots: tail slots of tiles ta..tb-1, head slot of tb.
 
+// Measured on C4 (85 long keys; the spike key has 649 slots, so each of its
+// 16 units walks 41 slots per thread): 15.8 us. 8 slots in flight (4 waves
+// per SIMD instead of 3): 15.4 us; units of 4 columns x 64 slices (64 units
+// for the spike key, 4x the units in all): 39 us, each unit paying its chain
+// of dependent loads (owner, end tile, slots) in turn.
 constexpr int FXU = 16;
 
 template <bool VEC>
@@ -616,9 +625,9 @@ __global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t n, int
   for (int64_t wk = blockIdx.x; wk < nunits; wk += gridDim.x) {
     const int64_t oi = wk / c16;
     const int chunk = (int)(wk - oi * c16);
-    const int64_t ta = owners[oi];
-    const int64_t p1 = min<int64_t>(ta * st + st, n);
-    const int key = skeys[p1 - 1];
+    const int2 ow = reinterpret_cast<const int2*>(owners)[oi];
+    const int64_t ta = ow.x;
+    const int key = ow.y;
     const int64_t tb = ((uint64_t)key < (uint64_t)len) ? end_tile[key] : -1;
     if (tb <= ta + 1 || tb >= stiles) {  // inconsistent: reported, nothing written
       if (threadIdx.x == 0) atomicOr(guard, 2);
@@ -789,11 +798,11 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   while (st > 16 && ceil_div(n, st) * chunks < 8 * (int64_t)cu_count()) st >>= 1;
   const int64_t stiles = ceil_div(n, st);
   // end tile per key and the owner list of long keys; partial rows
-  Workspace wsi(((size_t)len + (size_t)stiles) * sizeof(int));
+  Workspace wsi(((size_t)len + 1 + 2 * (size_t)stiles) * sizeof(int));
   Workspace wsp((size_t)2 * (size_t)stiles * (size_t)outer * (size_t)inner * sizeof(double));
   if (!wsi.p || !wsp.p) return fail_alloc("index_select_bwd: apply workspace");
   int* end_tile = wsi.as<int>();
-  int* owners = end_tile + len;
+  int* owners = end_tile + len + (len & 1);  // (tile, key) pairs, 8-byte aligned
   const int* ka = p.ka;
   const int* va = p.va;
   int* present = p.present;
