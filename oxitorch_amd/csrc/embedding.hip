@@ -37,10 +37,14 @@ namespace oxi {
 namespace {
 
 constexpr int BS = 256;
+// Rows per gather block. Measured in the cold step (the table's rows first
+// come from HBM): C4's gather 130.7 us at 2 rows, 123.8 at 4, 124.0 at 8;
+// C5's 24.3-24.6, 22.6-23.0 and 21.6 us. With the table in the Infinity
+// Cache (warm) 2 rows measured best (C4 90.2 against 92.7 us at 4).
 #ifndef OXI_GRPB
-#define OXI_GRPB 2
+#define OXI_GRPB 4
 #endif
-constexpr int GRPB = OXI_GRPB;  // rows per gather block
+constexpr int GRPB = OXI_GRPB;
 
 __device__ __forceinline__ int64_t wrap_id(int64_t id, int64_t len, bool& ok) {
   if (id < 0) id += len;
@@ -438,9 +442,16 @@ constexpr int ZR = OXI_SEG_ZR;  // zero rows per block
 #ifndef OXI_SEG_WPE
 #define OXI_SEG_WPE 5
 #endif
+// DB: the loads of the next SEG_U positions issue before the current ones
+// are added (two register sets, 141 VGPRs: 3 waves per SIMD). Measured in
+// the cold step: C4's embedding VJP 158.6 us against 164.9 single-buffered;
+// C5's 48.5 against 38.3 us (a small grid needs the occupancy), so it is
+// taken from DB_MIN_IDS ids on. At 4 waves per SIMD it spills (173 us);
+// 6 rows at 4 waves took 161.9 us, 4 rows at 5 waves 167.4.
+constexpr int64_t DB_MIN_IDS = 65536;
 
-template <bool VEC, bool NTS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE))) void seg_wave_k(
+template <bool VEC, bool NTS, bool DB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DB ? 3 : OXI_SEG_WPE))) void seg_wave_k(
     const float* __restrict__ g, int64_t outer, int64_t n, int64_t inner, int64_t len,
     const int* __restrict__ skeys, const int* __restrict__ perm, float* __restrict__ grad,
     double* __restrict__ part, const int* __restrict__ present, int* __restrict__ owners,
@@ -523,18 +534,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE
 #pragma unroll
     for (int q = 0; q < NC; ++q) accd[q] = 0.0;
     int start = first;
-    for (int i = first; i < cnt; i += SEG_U) {
-      V vals[SEG_U];
-#pragma unroll
-      for (int j = 0; j < SEG_U; ++j) {
-        vals[j] = V{};
-        const int pj = __builtin_amdgcn_readlane(my_pos, (i + j) & 63);  // uniform; used only if i + j < cnt
-        if (i + j < cnt && active && (uint64_t)pj < (uint64_t)n) {
-          const float* row = gb + (int64_t)pj * inner;
-          if constexpr (VEC) vals[j] = ld_stream(reinterpret_cast<const f4*>(row) + u);
-          else vals[j] = ld_stream(row + u);
-        }
-      }
+    auto consume = [&](V (&vals)[SEG_U], int i) {
 #pragma unroll
       for (int j = 0; j < SEG_U; ++j) {
         const int q = i + j;
@@ -568,6 +568,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OXI_SEG_WPE
           for (int c = 0; c < NC; ++c) accd[c] = 0.0;
           start = q + 1;
         }
+      }
+    };
+    if constexpr (DB) {
+      // Every load issues (its position clamped into the tile, an invalid
+      // one read as row 0 and zeroed), so each wait counts exactly the
+      // younger loads.
+      auto load_batch = [&](V (&v)[SEG_U], int i) {
+#pragma unroll
+        for (int j = 0; j < SEG_U; ++j) {
+          const int pj = __builtin_amdgcn_readlane(my_pos, min(i + j, cnt - 1));
+          const bool okp = (uint64_t)pj < (uint64_t)n;
+          const float* row = gb + (int64_t)(okp ? pj : 0) * inner;
+          V t = V{};
+          if (active) {
+            if constexpr (VEC) t = ld_stream(reinterpret_cast<const f4*>(row) + u);
+            else t = ld_stream(row + u);
+          }
+          v[j] = okp ? t : V{};
+        }
+      };
+      V va[SEG_U], vb[SEG_U];
+      if (first < cnt) load_batch(va, first);
+      for (int i = first; i < cnt;) {
+        load_batch(vb, i + SEG_U);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(va, i);
+        i += SEG_U;
+        if (i >= cnt) break;
+        load_batch(va, i + SEG_U);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(vb, i);
+        i += SEG_U;
+      }
+    } else {
+      for (int i = first; i < cnt; i += SEG_U) {
+        V vals[SEG_U];
+#pragma unroll
+        for (int j = 0; j < SEG_U; ++j) {
+          vals[j] = V{};
+          const int pj = __builtin_amdgcn_readlane(my_pos, (i + j) & 63);  // uniform; used only if i + j < cnt
+          if (i + j < cnt && active && (uint64_t)pj < (uint64_t)n) {
+            const float* row = gb + (int64_t)pj * inner;
+            if constexpr (VEC) vals[j] = ld_stream(reinterpret_cast<const f4*>(row) + u);
+            else vals[j] = ld_stream(row + u);
+          }
+        }
+        consume(vals, i);
       }
     }
     if (tail_ext) {  // the last run goes on into the next tile's first ext_len positions
@@ -818,15 +865,20 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   const int64_t blocks = seg_blocks + ceil_div(len, ZR);
   if (blocks >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many rows");
   const dim3 sg((unsigned)blocks), st256(256);
-  if (vec && nts)
-    seg_wave_k<true, true><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners, owner_count,
-                                                end_tile, st, stiles, (int)chunks, seg_blocks);
-  else if (vec)
-    seg_wave_k<true, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
-                                                 owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
-  else
-    seg_wave_k<false, false><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,
-                                                  owner_count, end_tile, st, stiles, (int)chunks, seg_blocks);
+  const bool db = n >= DB_MIN_IDS;
+#define OXI_SEG(VEC, NTS, DB)                                                                                     \
+  seg_wave_k<VEC, NTS, DB><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,     \
+                                                owner_count, end_tile, st, stiles, (int)chunks, seg_blocks)
+  if (vec && nts) {
+    if (db) OXI_SEG(true, true, true);
+    else OXI_SEG(true, true, false);
+  } else if (vec) {
+    if (db) OXI_SEG(true, false, true);
+    else OXI_SEG(true, false, false);
+  } else {
+    OXI_SEG(false, false, false);
+  }
+#undef OXI_SEG
   if (int rc = check_launch("index_select_bwd/segments")) return rc;
   const unsigned fb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(stiles * c16, 4 * (int64_t)cu_count()));
   if (vec)

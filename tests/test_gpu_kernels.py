@@ -436,12 +436,14 @@ def _exact_bwd(g, shape, dim, idx):
     return np.moveaxis(out, 0, dim)
 
 
-@pytest.mark.parametrize("case", ["skewed_outer", "one_key", "tile_runs", "two_hot_keys"])
+@pytest.mark.parametrize("case", ["skewed_outer", "one_key", "tile_runs", "two_hot_keys", "many_ids"])
 def test_index_select_bwd_run_shapes(hip, case):
     """Runs shorter than, equal to and far longer than the VJP's position
     tiles, on the scalar path (rows not a multiple of 4 floats) with several
-    outer slices, and on the vector path: values vs the oracle, long sums vs
-    float64, runs inside one aligned tile bit-exact, every call deterministic."""
+    outer slices, and on the vector path, below and from 65536 ids (where the
+    segment kernel double-buffers its loads): values vs the oracle, long sums
+    vs float64, runs inside one aligned tile bit-exact, every call
+    deterministic."""
     from oracle import ref
     say("index_select_bwd runs", case)
     r = rng(21)
@@ -455,10 +457,16 @@ def test_index_select_bwd_run_shapes(hip, case):
         shape, dim = (400, 96), 0
         idx = np.repeat(r.permutation(400)[:120], r.integers(10, 81, 120)).astype(np.int64)
         r.shuffle(idx)
-    else:                        # two hot keys plus a uniform tail, negative ids included
+    elif case == "two_hot_keys":  # two hot keys plus a uniform tail, negative ids included
         shape, dim = (2000, 32), 0
         idx = np.concatenate([np.full(3000, 5), np.full(2500, -1), r.integers(-2000, 2000, 4000)]).astype(np.int64)
         r.shuffle(idx)
+    else:                        # about 110k ids: runs of 1..150 positions, a hot key, negative ids
+        shape, dim = (3000, 64), 0
+        runs = np.repeat(r.permutation(3000)[:1200], r.integers(1, 151, 1200))
+        idx = np.concatenate([runs, np.full(20000, 7), r.integers(-3000, 0, 2000)]).astype(np.int64)
+        r.shuffle(idx)
+        assert idx.size >= 65536
     L = shape[dim]
     out_shape = list(shape)
     out_shape[dim] = idx.size
