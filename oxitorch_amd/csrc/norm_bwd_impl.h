@@ -29,7 +29,9 @@ __device__ __forceinline__ float rsum1(float v, float* lds) { return group_sum_o
 // it loads x and g non-temporally. Measured at C5's (16, 1024, 768), in the
 // warm step: since the dx rows are staged in LDS (nothing re-read through
 // L2), non-temporal loads take 33-34 us against 44 us with plain ones, whose
-// lines evict the next kernels' inputs. Earlier, with dx re-read from L2,
+// lines evict the next kernels' inputs. 512-thread blocks (8 rows a chunk,
+// half the barriers) took 39.6-40.0 us in the step against 37.0-37.4 us.
+// Earlier, with dx re-read from L2,
 // 256 threads measured 40.7 us with plain loads and 47.1 us with
 // non-temporal ones, 512 and 1024 threads 47.4 and 52.0 us.
 #ifndef OXI_LSUM_SPLIT_THREADS
