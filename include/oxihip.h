@@ -409,9 +409,15 @@ int oxi_scatter_rows_bwd(const float* g, int64_t rows, int64_t inner,
  * broadcast-expanded to `shape`): the x values at grid points whose mask value
  * is not zero, in row-major order of `shape`. As in the reference, which marks
  * unpicked points NaN and drops every NaN, a picked NaN of x is dropped too.
- * The output size depends on the data: the call waits for the device to count
- * the picks, then allocates `*out` (`*count` floats, NULL when none) with
- * oxi_hip_alloc; the caller frees it with oxi_hip_free. When `record` is not
+ * The output size depends on the data, so the call waits for the device's
+ * count of the picks. `*out` holds at least `*count` floats (NULL when none),
+ * allocated with oxi_hip_alloc; the caller frees it with oxi_hip_free. By
+ * default x is read once: the picks go to a buffer sized for every grid point
+ * (moved into one of `*count` floats when they fill at most a third of it),
+ * and the call returns once the count is known, while the last picks are
+ * still being stored (later calls on the library stream run after them).
+ * OXI_MASKED_SELECT_EXACT=1 counts first and allocates exactly `*count`
+ * floats, reading x twice. When `record` is not
  * NULL (device memory of oxi_masked_select_record_bytes bytes, 8-byte
  * aligned) it receives the selection's record, one bit per grid point plus
  * per-tile offsets, which oxi_masked_select_bwd reads in place of x and the

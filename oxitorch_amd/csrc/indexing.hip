@@ -480,7 +480,8 @@ __global__ __launch_bounds__(MB) void msel_write_k(Grid<1> g, const float* __res
 // bounded: a walk that polls `spin_limit` times without progress (a negative
 // limit: at once) raises the guard flag (bit 4) and its chunk stores no
 // picks; the call reports a failed last chunk, oxi_hip_sync any other. The
-// output holds room for every grid point.
+// output holds room for every grid point (the host moves picks that fill at
+// most a third of it into an exact-size buffer).
 constexpr uint64_t LB_AGG = 1ull << 62, LB_PRE = 2ull << 62, LB_VAL = (1ull << 62) - 1;
 #ifndef OXI_MSEL_CHUNK
 #define OXI_MSEL_CHUNK 4
@@ -957,6 +958,22 @@ int oxi_masked_select(const float* x, const int64_t* x_strides, const float* mas
     if (total == 0) {
       oxi_hip_free(big);
       return OXI_OK;
+    }
+    // Picks that fill at most a third of the grid-sized buffer move into an
+    // exact-size one (the copy queued after the kernel), so a sparse mask's
+    // result holds at most three times its picks' memory; if that allocation
+    // fails, the grid-sized buffer is kept.
+    if (total * 3 <= E) {
+      void* exact = nullptr;
+      if (oxi_hip_alloc(sizeof(float) * (size_t)total, &exact) == OXI_OK && exact) {
+        const hipError_t e = hipMemcpyAsync(exact, big, sizeof(float) * (size_t)total, hipMemcpyDeviceToDevice, st);
+        oxi_hip_free(e == hipSuccess ? big : exact);
+        if (e != hipSuccess) {
+          oxi_hip_free(big);
+          return fail_hip(e, "hipMemcpyAsync(masked_select)");
+        }
+        big = exact;
+      }
     }
     *out = static_cast<float*>(big);
     *count = total;

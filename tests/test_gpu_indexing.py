@@ -161,6 +161,32 @@ def test_masked_select_matches_oracle(hip, oracle, xs, ms, density, msel_path):
     got.free()
 
 
+@pytest.mark.parametrize("density,exact", [(0.1, True), (0.3, True), (0.6, False)])
+def test_masked_select_output_memory(hip, oracle, density, exact):
+    """The one pass's output: picks that fill at most a third of the grid
+    move into a buffer of their own size (the allocator's 512-byte or 2 MiB
+    rounding aside), denser ones keep the grid-sized buffer; the bits are the
+    oracle's either way."""
+    say("masked_select output memory", density)
+    r = rng(31)
+    shape = (1024, 2048)  # 8 MiB of x: the grid-sized buffer is 8 MiB
+    x = r.standard_normal(shape, dtype=np.float32)
+    m = (r.random(shape, dtype=np.float32) < density).astype(np.float32)
+    dx, dm = hip.DeviceArray.from_numpy(x), hip.DeviceArray.from_numpy(m)
+    hip.sync()
+    base = hip.memory_stats()[0]
+    got = hip.masked_select(dx, dm)
+    held = hip.memory_stats()[0] - base
+    bits_equal(got.numpy(), oracle.masked_select(x, m), f"masked_select density {density}")
+    picks = 4 * got.size
+    grid = 4 * x.size
+    if exact:
+        assert picks * 3 <= grid and held <= picks + (2 << 20), (held, picks)
+    else:
+        assert picks * 3 > grid and held >= grid, (held, grid)
+    got.free()
+
+
 def test_masked_select_strided_operands(hip, oracle, msel_path):
     """A transposed x and a broadcast column mask, through explicit strides."""
     say("masked_select strided")
