@@ -419,8 +419,9 @@ __global__ __launch_bounds__(SBS) void sort_scatter_k(const int64_t* __restrict_
 //    ends --
 //    and the tile where it starts joins the owner list while the tile where it
 //    ends records itself in end_tile[key]; seg_fixup_k adds the slots.
-// Blocks past the segment work write zero rows for keys that never occur
-// (ZR rows per block), so those writes overlap the gathers.
+// Zero rows for keys that never occur (ZR rows per block) are written by
+// blocks past the segment work, so those writes overlap the gathers, or, from
+// DB_MIN_IDS ids on, by blocks past the fix-up work (see the launch).
 
 // Rows in flight per lane, and the longest segment tile (below). Measured on
 // C4 (131072 Zipf ids, 1024-float rows), C4 step: 8 and 64 take 252 us;
@@ -450,6 +451,26 @@ constexpr int ZR = OXI_SEG_ZR;  // zero rows per block
 // 6 rows at 4 waves took 161.9 us, 4 rows at 5 waves 167.4.
 constexpr int64_t DB_MIN_IDS = 65536;
 
+// The dW rows of keys that never occur, ZR per block (block zb of the
+// zero-row blocks), written with zeros.
+template <bool VEC, bool NTS>
+__device__ __forceinline__ void zero_rows(int64_t zb, const int* __restrict__ present, float* __restrict__ grad,
+                                          int64_t outer, int64_t len, int64_t inner) {
+  const int64_t units = VEC ? inner / 4 : inner;
+  const int64_t v0 = zb * ZR;
+  for (int r = 0; r < ZR; ++r) {
+    const int64_t v = v0 + r;
+    if (v >= len || present[v]) continue;
+    for (int64_t o = 0; o < outer; ++o) {
+      float* dst = grad + (o * len + v) * inner;
+      for (int64_t c = threadIdx.x; c < units; c += 256) {
+        if constexpr (VEC) st_stream<NTS>(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + c);
+        else st_stream<NTS>(0.f, dst + c);
+      }
+    }
+  }
+}
+
 template <bool VEC, bool NTS, bool DB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DB ? 3 : OXI_SEG_WPE))) void seg_wave_k(
     const float* __restrict__ g, int64_t outer, int64_t n, int64_t inner, int64_t len,
@@ -460,18 +481,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DB ? 3 : OX
   using V = typename std::conditional<VEC, f4, float>::type;
   const int64_t units = VEC ? inner / 4 : inner;
   if ((int64_t)blockIdx.x >= seg_blocks) {
-    const int64_t v0 = ((int64_t)blockIdx.x - seg_blocks) * ZR;
-    for (int r = 0; r < ZR; ++r) {
-      const int64_t v = v0 + r;
-      if (v >= len || present[v]) continue;
-      for (int64_t o = 0; o < outer; ++o) {
-        float* dst = grad + (o * len + v) * inner;
-        for (int64_t c = threadIdx.x; c < units; c += 256) {
-          if constexpr (VEC) st_stream<NTS>(f4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f4*>(dst) + c);
-          else st_stream<NTS>(0.f, dst + c);
-        }
-      }
-    }
+    zero_rows<VEC, NTS>((int64_t)blockIdx.x - seg_blocks, present, grad, outer, len, inner);
     return;
   }
   const int lane = threadIdx.x & 63;
@@ -658,18 +668,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DB ? 3 : OX
 // of dependent loads (owner, end tile, slots) in turn.
 constexpr int FXU = 16;
 
-template <bool VEC>
+template <bool VEC, bool NTS>
 __global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t n, int64_t inner, int64_t len, int st,
-                                                   int64_t stiles, const int* __restrict__ skeys,
-                                                   const int* __restrict__ owners, const int* __restrict__ owner_count,
+                                                   int64_t stiles, const int* __restrict__ owners,
+                                                   const int* __restrict__ owner_count,
                                                    const int* __restrict__ end_tile, const double* __restrict__ part,
-                                                   float* __restrict__ grad, int c16, int* guard) {
+                                                   float* __restrict__ grad, int c16, int* guard,
+                                                   const int* __restrict__ present, int64_t fb) {
+  if ((int64_t)blockIdx.x >= fb) {  // the zero rows, behind the long keys' latency-bound sums
+    zero_rows<VEC, NTS>((int64_t)blockIdx.x - fb, present, grad, outer, len, inner);
+    return;
+  }
   constexpr int NC = VEC ? 4 : 1;
   __shared__ double red[4][16][NC];
   const int64_t units = VEC ? inner / 4 : inner;
   const int sl = threadIdx.x >> 4, c = threadIdx.x & 15, w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t nunits = (int64_t)(*owner_count) * c16;
-  for (int64_t wk = blockIdx.x; wk < nunits; wk += gridDim.x) {
+  for (int64_t wk = blockIdx.x; wk < nunits; wk += fb) {
     const int64_t oi = wk / c16;
     const int chunk = (int)(wk - oi * c16);
     const int2 ow = reinterpret_cast<const int2*>(owners)[oi];
@@ -862,10 +877,19 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   // the rows of g stream through the cache while dW is written: decide on
   // the launch's whole traffic, not on dW alone
   const bool nts = nt_stores((total_out + outer * n * inner) * 4);
-  const int64_t blocks = seg_blocks + ceil_div(len, ZR);
-  if (blocks >= ((int64_t)1 << 31)) return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many rows");
-  const dim3 sg((unsigned)blocks), st256(256);
+  // From DB_MIN_IDS ids on the zero rows are written by the fix-up launch,
+  // behind its latency-bound sums: C4's VJP 160.8-161.0 us against
+  // 163.2-163.6 with them in the segment launch. Below, the segment launch
+  // writes them, where they hide behind its gathers: there C5's VJP took
+  // 46.6-46.9 us with them in the fix-up against 38.3-38.7.
   const bool db = n >= DB_MIN_IDS;
+  const int64_t zblocks = ceil_div(len, ZR);
+  const int64_t fb = std::max<int64_t>(1, std::min<int64_t>(stiles * c16, 4 * (int64_t)cu_count()));
+  const int64_t blocks = seg_blocks + (db ? 0 : zblocks);
+  const int64_t fblocks = fb + (db ? zblocks : 0);
+  if (blocks >= ((int64_t)1 << 31) || fblocks >= ((int64_t)1 << 31))
+    return fail(OXI_INVALID_ARGUMENT, "index_select_bwd: too many rows");
+  const dim3 sg((unsigned)blocks), st256(256);
 #define OXI_SEG(VEC, NTS, DB)                                                                                     \
   seg_wave_k<VEC, NTS, DB><<<sg, st256, 0, s>>>(g, outer, n, inner, len, ka, va, grad, part, present, owners,     \
                                                 owner_count, end_tile, st, stiles, (int)chunks, seg_blocks)
@@ -880,13 +904,14 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
   }
 #undef OXI_SEG
   if (int rc = check_launch("index_select_bwd/segments")) return rc;
-  const unsigned fb = (unsigned)std::max<int64_t>(1, std::min<int64_t>(stiles * c16, 4 * (int64_t)cu_count()));
-  if (vec)
-    seg_fixup_k<true><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
-                                         grad, (int)c16, guard_flag());
-  else
-    seg_fixup_k<false><<<fb, 256, 0, s>>>(outer, n, inner, len, st, stiles, ka, owners, owner_count, end_tile, part,
-                                          grad, (int)c16, guard_flag());
+#define OXI_FIX(VEC, NTS)                                                                                        \
+  seg_fixup_k<VEC, NTS><<<dim3((unsigned)fblocks), st256, 0, s>>>(outer, n, inner, len, st, stiles, owners,      \
+                                                                 owner_count, end_tile, part, grad, (int)c16,    \
+                                                                 guard_flag(), present, fb)
+  if (vec && nts) OXI_FIX(true, true);
+  else if (vec) OXI_FIX(true, false);
+  else OXI_FIX(false, false);
+#undef OXI_FIX
   return check_launch("index_select_bwd/fixup");
 }
 

@@ -436,12 +436,14 @@ def _exact_bwd(g, shape, dim, idx):
     return np.moveaxis(out, 0, dim)
 
 
-@pytest.mark.parametrize("case", ["skewed_outer", "one_key", "tile_runs", "two_hot_keys", "many_ids"])
+@pytest.mark.parametrize("case", ["skewed_outer", "one_key", "tile_runs", "two_hot_keys", "many_ids",
+                                  "many_ids_no_long_run"])
 def test_index_select_bwd_run_shapes(hip, case):
     """Runs shorter than, equal to and far longer than the VJP's position
     tiles, on the scalar path (rows not a multiple of 4 floats) with several
     outer slices, and on the vector path, below and from 65536 ids (where the
-    segment kernel double-buffers its loads): values vs the oracle, long sums
+    segment kernel double-buffers its loads and the fix-up launch writes the
+    zero rows, with and without long runs): values vs the oracle, long sums
     vs float64, runs inside one aligned tile bit-exact, every call
     deterministic."""
     from oracle import ref
@@ -461,6 +463,10 @@ def test_index_select_bwd_run_shapes(hip, case):
         shape, dim = (2000, 32), 0
         idx = np.concatenate([np.full(3000, 5), np.full(2500, -1), r.integers(-2000, 2000, 4000)]).astype(np.int64)
         r.shuffle(idx)
+    elif case == "many_ids_no_long_run":  # 70000 ids over 200000 rows: no run spans three tiles,
+        shape, dim = (200000, 16), 0      # so the fix-up launch only writes the zero rows
+        idx = r.integers(0, 200000, 70000).astype(np.int64)
+        assert np.bincount(idx).max() < 64
     else:                        # about 110k ids: runs of 1..150 positions, a hot key, negative ids
         shape, dim = (3000, 64), 0
         runs = np.repeat(r.permutation(3000)[:1200], r.integers(1, 151, 1200))
