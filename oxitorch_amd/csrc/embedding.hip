@@ -669,7 +669,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DB ? 3 : OX
 constexpr int FXU = 16;
 
 template <bool VEC, bool NTS>
-__global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t n, int64_t inner, int64_t len, int st,
+__global__ __launch_bounds__(256) void seg_fixup_k(int64_t outer, int64_t inner, int64_t len,
                                                    int64_t stiles, const int* __restrict__ owners,
                                                    const int* __restrict__ owner_count,
                                                    const int* __restrict__ end_tile, const double* __restrict__ part,
@@ -905,7 +905,7 @@ int apply_plan(const SortPlan& p, const float* g, int64_t outer, int64_t inner, 
 #undef OXI_SEG
   if (int rc = check_launch("index_select_bwd/segments")) return rc;
 #define OXI_FIX(VEC, NTS)                                                                                        \
-  seg_fixup_k<VEC, NTS><<<dim3((unsigned)fblocks), st256, 0, s>>>(outer, n, inner, len, st, stiles, owners,      \
+  seg_fixup_k<VEC, NTS><<<dim3((unsigned)fblocks), st256, 0, s>>>(outer, inner, len, stiles, owners,              \
                                                                  owner_count, end_tile, part, grad, (int)c16,    \
                                                                  guard_flag(), present, fb)
   if (vec && nts) OXI_FIX(true, true);

@@ -216,7 +216,6 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         if (k * TPR + t < h4) {
-          const int c = k * TPR + t;
           f4 yv = LN ? (xt.v[k] - mu) * inv : xt.v[k] * inv;
           if (w) yv = yv * w_at(k);
           if (LN && b) yv = yv + b_at(k);
@@ -332,7 +331,7 @@ void norm_bwd_k(const float* __restrict__ x, const float* __restrict__ w,
       }
       __syncthreads();  // the chunk's dx rows are staged
       const int n = min(GPB, lead - ck_p * GPB);
-      if (threadIdx.x < h4) {
+      if ((int)threadIdx.x < h4) {
         if (ck_p == 0) acc = zero;
         for (int j = 0; j < n; ++j) acc = acc + stage[j * h4 + threadIdx.x];
         if (ck_p == nchunk - 1) st_stream<NTS>(acc, lsum4 + p_p * h4 + threadIdx.x);
