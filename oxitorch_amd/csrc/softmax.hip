@@ -299,6 +299,8 @@ __global__ __launch_bounds__(CE_BS) void ce_fwd_k(const float* __restrict__ logi
 // Measured at C3 (8192 x 32000), two-exp form: 512 x 16 ran the forward with
 // the gradient in 380 us (1024 x 8, held to one block per CU by its 68 VGPRs:
 // 476 us; 256 x 32: 417 us) and the forward alone in 181 us (streaming: 174 us).
+// With one exp, the restructured loops below and 60 VGPRs, 1024 x 8 runs two
+// blocks per CU and is the faster shape at C3 (see ce_forward).
 // TAIL1: the row fills all but the last of a thread's NV float4 slots
 // ((NV - 1) * RT < C / 4 <= NV * RT, as at C3's 32000 classes), so only slot
 // NV - 1 is bounds-checked. The hot loops take the minimum over every logit;
@@ -625,9 +627,19 @@ int ce_forward(const char* what, const float* logits, const int64_t* targets, fl
   const int vec = (c % 4 == 0 && aligned16({logits})) ? 1 : 0;
   const int64_t c4 = c / 4;
   // (threads, float4s a thread) of the register-row kernel: 16 float4s a
-  // thread, as few threads as the row needs
-  int rt = 0;
-  if (vec) rt = c4 <= 1024 ? 64 : c4 <= 2048 ? 128 : c4 <= 4096 ? 256 : c4 <= 8192 ? 512 : c4 <= 16384 ? 1024 : 0;
+  // thread, as few threads as the row needs; rows of 4097 to 8192 float4s
+  // take 1024 threads of 8 (60 VGPRs, two blocks per CU): C3's step 362.6
+  // and 362.7 us against 367.3 and 367.9 at 512 x 16 on one box.
+  int rt = 0, nv = 16;
+  if (vec) {
+    if (c4 > 4096 && c4 <= 8192) {
+      rt = 1024;
+      nv = 8;
+    } else {
+      for (int t = 64; t <= 1024 && !rt; t *= 2)
+        if (c4 <= (int64_t)t * 16) rt = t;
+    }
+  }
   if (dunit && !(rt && aligned16({dunit})))
     return fail(OXI_NOT_IMPLEMENTED, "%s: rows of %lld classes do not take the one-pass kernel (c %% 4 != 0, more "
                 "than 65536 classes or unaligned)", what, (long long)c);
@@ -636,27 +648,27 @@ int ce_forward(const char* what, const float* logits, const int64_t* targets, fl
   const dim3 grid((unsigned)n);
   float* pk = picked.as<float>();
   const bool nt = nt_stores(n * c * 4);  // the gradient's stores
-  switch (rt) {
-#define OXI_CE_GO(RT, GRAD, NTS, TAIL1)                                                                    \
-  ce_fwd_rows_k<RT, 16, GRAD, NTS, TAIL1><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, \
+  switch (rt * 100 + nv) {
+#define OXI_CE_GO(RT, NV, GRAD, NTS, TAIL1)                                                                \
+  ce_fwd_rows_k<RT, NV, GRAD, NTS, TAIL1><<<grid, dim3(RT), 0, stream()>>>(logits, targets, lse, pk, dunit, n, \
                                                                           (int)c, guard_flag())
-#define OXI_CE_ROWS(RT)                                                                                     \
-  case RT:                                                                                                  \
-    if (c4 > 15 * RT) {                                                                                     \
-      if (!dunit) OXI_CE_GO(RT, false, false, true);                                                        \
-      else if (nt) OXI_CE_GO(RT, true, true, true);                                                         \
-      else OXI_CE_GO(RT, true, false, true);                                                                \
+#define OXI_CE_ROWS(RT, NV)                                                                                 \
+  case RT * 100 + NV:                                                                                       \
+    if (c4 > (NV - 1) * RT) {                                                                               \
+      if (!dunit) OXI_CE_GO(RT, NV, false, false, true);                                                    \
+      else if (nt) OXI_CE_GO(RT, NV, true, true, true);                                                     \
+      else OXI_CE_GO(RT, NV, true, false, true);                                                            \
     } else {                                                                                                \
-      if (!dunit) OXI_CE_GO(RT, false, false, false);                                                       \
-      else if (nt) OXI_CE_GO(RT, true, true, false);                                                        \
-      else OXI_CE_GO(RT, true, false, false);                                                               \
+      if (!dunit) OXI_CE_GO(RT, NV, false, false, false);                                                   \
+      else if (nt) OXI_CE_GO(RT, NV, true, true, false);                                                    \
+      else OXI_CE_GO(RT, NV, true, false, false);                                                           \
     }                                                                                                       \
     break;
-    OXI_CE_ROWS(64)
-    OXI_CE_ROWS(128)
-    OXI_CE_ROWS(256)
-    OXI_CE_ROWS(512)
-    OXI_CE_ROWS(1024)
+    OXI_CE_ROWS(64, 16)
+    OXI_CE_ROWS(128, 16)
+    OXI_CE_ROWS(256, 16)
+    OXI_CE_ROWS(1024, 8)
+    OXI_CE_ROWS(1024, 16)
 #undef OXI_CE_ROWS
 #undef OXI_CE_GO
     default:
