@@ -24,7 +24,8 @@ writes the gradient for loss.backward()'s seed 1, so its backward launches
 nothing.
 
 The main figure (`ms_per_step`, `value`) is the slower of two medians over
-K steps each (after W untimed warmup steps):
+K steps each (after W untimed warmup steps and about a quarter of a second of
+untimed steps, so that the GPU is back at its steady clocks):
 - cold: every step is preceded by an untimed flush of a 512 MiB scratch buffer
   (twice the 256 MB Infinity Cache), written and then read back, so the step
   reads its inputs from HBM and the cache holds no dirty lines (`--flush
@@ -82,6 +83,7 @@ import time
 import numpy as np
 
 PEAK_HBM_GBS = 8000.0
+SETTLE_S = 0.25  # untimed steps before a config's timed ones, in seconds
 MIB = 1 << 20
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -1150,9 +1152,10 @@ def _rate(nbytes, ms):
 def run_config(hip, key, args, flush):
     """Everything measured for one config; returns (compact block, detail).
 
-    W untimed warmup steps, then K cold and K warm timed steps (the graded
-    figure is the slower median), then K steps with per-call events under
-    the graded protocol, then the other measurements."""
+    W untimed warmup steps and about SETTLE_S s of untimed steps, then K
+    cold and K warm timed steps (the main figure is the slower median),
+    then K steps with per-call events under the graded protocol, then the
+    other measurements."""
     log(f"[{key}] building workload")
     wl = WORKLOADS[key](hip)
     kernels = wl.kernels()
@@ -1163,6 +1166,16 @@ def run_config(hip, key, args, flush):
         for _, fn, _ in kernels:
             fn()
     hip.sync()
+    # untimed steps for about SETTLE_S more: the host work before a config
+    # (building it, the previous config's CPU baseline) leaves the GPU idle
+    # for seconds, and a few warmup steps do not bring it back to its steady
+    # clocks (default runs had measured C2's warm step 8-30 us slower than
+    # runs of C2 alone)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _, fn, _ in kernels:
+            fn()
+        hip.sync()
     # cold: each step after a flush (inputs from HBM, a clean cache); warm:
     # back-to-back steps, each also paying the previous step's write-backs
     log(f"[{key}] timing {args.steps} cold-MALL steps")
