@@ -44,13 +44,13 @@ __device__ __forceinline__ float rsum1(float v, float* lds) { return group_sum_o
 
 // FULL: rows of exactly TPR * NV float4s (H = 4 * TPR * NV), a compile-time
 // row length: no padding lanes, no bounds checks.
-template <int TPR, int NV, bool LN, bool NTS, bool FULL>
-__global__ __launch_bounds__((row_block_threads(TPR))) void norm_fwd_k(const float* __restrict__ x, const float* __restrict__ w,
+// NT: threads per block, row_block_threads(TPR) or, for one-wave rows, 1024.
+template <int TPR, int NV, bool LN, bool NTS, bool FULL, int NT>
+__global__ __launch_bounds__(NT) void norm_fwd_k(const float* __restrict__ x, const float* __restrict__ w,
                                                  const float* __restrict__ b, float* __restrict__ y,
                                                  float* __restrict__ mean, float* __restrict__ rstd,
                                                  int64_t rows, int H_arg, float eps) {
   const int H = FULL ? 4 * TPR * NV : H_arg;
-  constexpr int NT = row_block_threads(TPR);
   constexpr int GPB = NT / TPR;
   __shared__ float lds[2 * (NT / 64)];  // mean, then variance
   const int t = threadIdx.x % TPR;
@@ -140,20 +140,34 @@ __global__ __launch_bounds__(BS) void norm_fwd_loop_k(const float* __restrict__ 
 template <bool LN, bool NTS>
 void launch_fwd_cfg(int cfg, hipStream_t s, const float* x, const float* w, const float* b, float* y, float* mean,
                     float* rstd, int64_t rows, int h, float eps) {
+#define OXI_FWD_NT(TPR, NV, NT)                                                                            \
+  if (h == 4 * TPR * NV)                                                                                   \
+    norm_fwd_k<TPR, NV, LN, NTS, true, NT><<<dim3((unsigned)ceil_div(rows, NT / TPR)), dim3(NT), 0, s>>>(   \
+        x, w, b, y, mean, rstd, rows, h, eps);                                                             \
+  else                                                                                                     \
+    norm_fwd_k<TPR, NV, LN, NTS, false, NT><<<dim3((unsigned)ceil_div(rows, NT / TPR)), dim3(NT), 0, s>>>(  \
+        x, w, b, y, mean, rstd, rows, h, eps);
 #define OXI_FWD(TPR, NV)                                                                                   \
   case TPR * 10 + NV:                                                                                      \
-    if (h == 4 * TPR * NV)                                                                                 \
-      norm_fwd_k<TPR, NV, LN, NTS, true><<<dim3((unsigned)ceil_div(rows, row_block_threads(TPR) / TPR)),   \
-                                           dim3(row_block_threads(TPR)), 0, s>>>(x, w, b, y, mean, rstd, rows, h, eps); \
-    else                                                                                                   \
-      norm_fwd_k<TPR, NV, LN, NTS, false><<<dim3((unsigned)ceil_div(rows, row_block_threads(TPR) / TPR)),  \
-                                            dim3(row_block_threads(TPR)), 0, s>>>(x, w, b, y, mean, rstd, rows, h, eps); \
+    OXI_FWD_NT(TPR, NV, row_block_threads(TPR))                                                            \
+    break;
+  // One-wave rows: 16 to a block when that leaves at most one block per CU
+  // (4096 rows of 768 floats: C1's rms_norm_fwd 6.8 us against 7.3 with 4
+  // to a block); with more rows 4 to a block (C5's 16384 rows: 18.4-18.6 us
+  // against 19.4-19.7 at 16).
+#define OXI_FWD1(NV)                                                                                       \
+  case 640 + NV:                                                                                           \
+    if (rows <= 16 * (int64_t)cu_count()) {                                                                \
+      OXI_FWD_NT(64, NV, 1024)                                                                             \
+    } else {                                                                                               \
+      OXI_FWD_NT(64, NV, row_block_threads(64))                                                            \
+    }                                                                                                      \
     break;
   switch (cfg) {
-    OXI_FWD(64, 1)
-    OXI_FWD(64, 2)
-    OXI_FWD(64, 3)
-    OXI_FWD(64, 4)
+    OXI_FWD1(1)
+    OXI_FWD1(2)
+    OXI_FWD1(3)
+    OXI_FWD1(4)
     OXI_FWD(256, 2)
     OXI_FWD(256, 4)
     OXI_FWD(512, 2)
@@ -162,6 +176,8 @@ void launch_fwd_cfg(int cfg, hipStream_t s, const float* x, const float* w, cons
       norm_fwd_loop_k<LN><<<dim3((unsigned)rows), dim3(BS), 0, s>>>(x, w, b, y, mean, rstd, rows, h, eps);
   }
 #undef OXI_FWD
+#undef OXI_FWD1
+#undef OXI_FWD_NT
 }
 
 template <bool LN>
