@@ -521,18 +521,22 @@ __global__ __launch_bounds__(BS) void norm_bwd_loop_k(const float* __restrict__ 
 }
 
 // out[c] = sum over partial rows b (fixed order, float64) of part[b][c].
-// A block owns FIN_C columns; its threads form FIN_S slices of FIN_C lanes,
-// slice s summing the rows b = s, s + FIN_S, ... (FIN_U loads in flight: up
-// to 1024 partial rows in one round), then eight threads per column add the
-// slice sums in slice order in two steps. blockIdx.y selects the dw (0) or db
-// (1) plane. Measured at C5's (1024 partial rows, 768 columns): 64 columns
-// x 16 slices per block (12 blocks) took 5.6-6.7 us.
+// A block owns FIN_C columns; its threads form FS slices of FIN_C lanes,
+// slice s summing the rows b = s, s + FS, ... (FIN_U loads in flight: up to
+// FS * FIN_U partial rows in one round), then eight threads per column add
+// the slice sums in slice order in two steps. blockIdx.y selects the dw (0)
+// or db (1) plane. FS = 16 (256-thread blocks) when the partial rows fit one
+// round, else 64: C1's rms_norm VJP (256 partial rows) 11.7-11.8 us in the
+// step against 12.2 at 64 slices; C5's positional-sum VJP (1024 partial
+// rows) 38.3-38.5 us at 64 slices against 39.0-39.1 at 16. Earlier, 64
+// columns x 16 slices per block took 5.6-6.7 us at C5.
 constexpr int FIN_C = 16;
-constexpr int FIN_S = 64;
 constexpr int FIN_U = 16;
 
-__global__ __launch_bounds__(FIN_C * FIN_S) void col_finish_k(const float* __restrict__ part, int nb, int H,
-                                                            float* __restrict__ out0, float* __restrict__ out1) {
+template <int FS>
+__global__ __launch_bounds__(FIN_C * FS) void col_finish_k(const float* __restrict__ part, int nb, int H,
+                                                         float* __restrict__ out0, float* __restrict__ out1) {
+  constexpr int FIN_S = FS;
   float* out = blockIdx.y ? out1 : out0;
   if (!out) return;
   const float* p = part + (int64_t)blockIdx.y * nb * H;
@@ -678,8 +682,11 @@ int launch_bwd(const float* x, const float* w, const float* b, const float* mean
   int rc = check_launch(LN ? "layer_norm_bwd" : "rms_norm_bwd");
   if (rc != OXI_OK) return rc;
   if (need_part) {
-    col_finish_k<<<dim3((unsigned)ceil_div(H, FIN_C), LN ? 2 : 1), dim3(FIN_C * FIN_S), 0, s>>>(
-        part, (int)nblk, h, dw, LN ? db : nullptr);
+    const dim3 fg((unsigned)ceil_div(H, FIN_C), LN ? 2 : 1);
+    if (nblk <= 16 * FIN_U)
+      col_finish_k<16><<<fg, dim3(FIN_C * 16), 0, s>>>(part, (int)nblk, h, dw, LN ? db : nullptr);
+    else
+      col_finish_k<64><<<fg, dim3(FIN_C * 64), 0, s>>>(part, (int)nblk, h, dw, LN ? db : nullptr);
     rc = check_launch("norm_param_grad_finish");
   }
   return rc;
