@@ -250,7 +250,8 @@ def test_cross_entropy(hip, n, c):
 
 
 @pytest.mark.parametrize("n,c", [(2, 4), (64, 1000), (7, 36), (33, 8196), (256, 32000), (5, 65536), (3, 4100),
-                                 (9, 8192), (4, 16388), (8192, 32000)])
+                                 (9, 8192), (4, 16388), (3, 28672), (3, 28676), (3, 32768), (3, 32772),
+                                 (8192, 32000)])
 def test_cross_entropy_fwd_grad_against_the_oracle(hip, n, c):
     """The forward that also writes the gradient for an upstream 1 writes the
     loss and lse of oxi_cross_entropy_fwd bit for bit, and dlogits as the
